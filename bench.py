@@ -1,0 +1,206 @@
+"""Benchmark: MuSc mutual scoring of the default pool on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config pool|super_fast|plumbing]
+                    [--no-cpu-baseline]
+
+One step is one pass of the hot path over the whole synthetic pool, inputs
+resident in HBM: LNAMD for every (layer, radius) with the fused L2
+normalisation, the 12 MSM calls (4 layers x 3 radii) and the epilogue
+(layer/radius means, bilinear upsampling to 518 x 518, image scores).  This is
+N=83 images x 4 layers x 1369 patches x 1024 channels,
+radii 1/3/5, all 83*82 image pairs, trimmed ranks [0, 24).
+
+`value` = N * K / (wall time of the K timed steps), images/s.  The roofline
+object covers the dominant kernel, the MSM pair-minima kernel (fp32 MFMA):
+algorithmic FLOP per launch = C * P^2 * N * (N-1) (each unordered cross-image
+patch pair's 2C-FLOP dot product counted once), divided by that kernel's
+average duration from torch.cuda (HIP) events recorded around every launch in
+the timed region on the stream it runs on.  The CPU baseline is the oracle's
+restatement of the reference's original torch backend, timed on a bounded
+sample on this host and extrapolated to the whole job.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, 'musc-gpu_amd')):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+FP32_MFMA_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBPS = 8000.0
+
+CONFIGS = {
+    # name: (n, layers, tokens, c, radii, image_size, description)
+    'pool': (83, 4, 1370, 1024, [1, 3, 5], 518,
+             'default MSM pool: N=83 x 4 layers x 37x37 patches x 1024, radii 1/3/5, all pairs'),
+    'plumbing': (8, 1, 1370, 1024, [1], 518, 'plumbing pool: N=8 x 1 layer x 37x37 x 1024, radius 1'),
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(tokens_cpu, pools_gpu, r_list, image_size, gpu_scores_rl0, budget_s: float = 20.0):
+    """Time the oracle (torch CPU restatement of the original backend) on a bounded sample.
+
+    Sample: LNAMD (Unfold path) for one batch of 4 images, every layer and radius;
+    compute_scores_fast for a few query images of one (radius, layer) pool; the
+    epilogue on the full score tensor.  Extrapolated to the whole job.
+    """
+    import torch
+    from oracle import epilogue as oe
+    from oracle import lnamd as ol
+    from oracle import msm as om
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    n = tokens_cpu[0].shape[0]
+    n_layers = len(tokens_cpu)
+    batch = 4
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        for r in r_list:
+            f = ol.lnamd_embed([t[:batch] for t in tokens_cpu], r)
+            ol.l2_normalise(f)
+    t_lnamd_batch = time.perf_counter() - t0
+    z = pools_gpu[0, 0].cpu()
+    q_times, errs = [], []
+    queries = [0, n // 2, n - 1, 1, n // 3, 2 * n // 3, n - 2, 5]
+    spent = 0.0
+    for i in queries:
+        t1 = time.perf_counter()
+        ref = om.compute_scores_fast(z, i).double()
+        dt = time.perf_counter() - t1
+        q_times.append(dt)
+        spent += dt
+        errs.append((ref - gpu_scores_rl0[i]).abs().max().item())
+        if spent > budget_s and len(q_times) >= 2:
+            break
+    t_query = sum(q_times) / len(q_times)
+    fake = [[torch.rand((n, z.shape[0]), dtype=torch.float64) for _ in range(n_layers)] for _ in r_list]
+    t2 = time.perf_counter()
+    oe.maps_and_scores(fake, image_size)
+    t_epi = time.perf_counter() - t2
+    n_batches = (n + batch - 1) // batch
+    total = n_batches * t_lnamd_batch + len(r_list) * n_layers * n * t_query + t_epi
+    return {
+        'value': n / total,
+        'unit': 'images/s',
+        'cores': threads,
+        'kind': 'port',
+        'sample': (f'oracle torch-CPU restatement of the original backend: LNAMD Unfold path on {batch} images x '
+                   f'{n_layers} layers x radii {r_list} ({t_lnamd_batch:.2f} s), compute_scores_fast on '
+                   f'{len(q_times)} query images of one (radius, layer) pool ({t_query:.2f} s each), epilogue '
+                   f'({t_epi:.2f} s); extrapolated to {n_batches} LNAMD batches + '
+                   f'{len(r_list) * n_layers * n} query images'),
+        'extrapolated_seconds': total,
+        'sampled_query_max_abs_err_vs_gpu': max(errs),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split('\n')[0])
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=5)
+    ap.add_argument('--warmup', type=int, default=1)
+    ap.add_argument('--config', choices=sorted(CONFIGS), default='pool')
+    ap.add_argument('--seed', type=int, default=42)
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f'bench.py measures one GPU only: this build has no multi-GPU path (--gpus {args.gpus} requested). '
+              'Run with --gpus 1.', file=sys.stderr)
+        return 2
+
+    import torch
+    from musc_hip import pipeline, synthetic
+    from musc_hip import _runtime as rt
+
+    if not torch.cuda.is_available():
+        print('bench.py needs a ROCm GPU', file=sys.stderr)
+        return 2
+    ok, reason = rt.available()
+    if not ok:
+        print(reason, file=sys.stderr)
+        return 2
+    dev = torch.device('cuda:0')
+    n, n_layers, n_tok, c, r_list, image_size, desc = CONFIGS[args.config]
+    p = n_tok - 1
+    log(f'[bench] generating {args.config} tokens (seed {args.seed})')
+    if args.config == 'plumbing':
+        tokens_cpu = [synthetic.plumbing_tokens(n, n_tok, c, seed=args.seed)]
+    else:
+        tokens_cpu = synthetic.pool_tokens(n, n_layers, n_tok, c, seed=args.seed)
+    tokens = [t.to(dev) for t in tokens_cpu]
+    torch.cuda.synchronize()
+
+    for w in range(args.warmup):
+        pipeline.score_pool(tokens, r_list, image_size)
+        torch.cuda.synchronize()
+        log(f'[bench] warmup step {w + 1}/{args.warmup} done')
+
+    timing: dict = {}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        maps, img = pipeline.score_pool(tokens, r_list, image_size, timing=timing)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    log(f'[bench] {args.steps} timed steps in {elapsed:.3f} s')
+
+    pair_ms = [a.elapsed_time(b) for a, b in timing['pairs']]
+    lnamd_ms = [a.elapsed_time(b) for a, b in timing['lnamd']]
+    pair_avg_s = sum(pair_ms) / len(pair_ms) / 1e3
+    flop_per_launch = float(c) * p * p * n * (n - 1)
+    achieved_tflops = flop_per_launch / pair_avg_s / 1e12
+    lnamd_bytes = 4.0 * n * n_layers * (n_tok * c + len(r_list) * p * c)   # 1 read + R writes (fp32)
+    lnamd_avg_s = sum(lnamd_ms) / len(lnamd_ms) / 1e3
+    lnamd_gbps = lnamd_bytes / lnamd_avg_s / 1e9
+
+    result = {
+        'metric': 'MSM pool images/sec + fp32 MFMA TFLOP/s (% peak), 83-image 37x37x1024 pool',
+        'value': n * args.steps / elapsed,
+        'unit': 'images/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': elapsed / args.steps * 1e3,
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'fp32',
+        'data': 'synthetic (seeded N(0,1) tokens + shared per-layer offset, L2-normalised; resident in HBM)',
+        'config': {'workload': desc, 'images': n, 'layers': n_layers, 'patches': p, 'channels': c,
+                   'radii': r_list, 'image_size': image_size, 'rank_window': [0, int((n - 1) * 0.3)],
+                   'seed': args.seed},
+        'roofline': {'bound': 'mfma', 'kernel': 'msm_pair_min_kernel',
+                     'achieved': achieved_tflops, 'peak': FP32_MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
+                     'frac': achieved_tflops / FP32_MFMA_PEAK_TFLOPS, 'traffic': None,
+                     'flop_per_launch': flop_per_launch, 'avg_launch_ms': pair_avg_s * 1e3,
+                     'launches': len(pair_ms)},
+        'kernels': {'lnamd_all_radii': {'bound': 'hbm', 'achieved': lnamd_gbps, 'peak': HBM_PEAK_GBPS,
+                                        'unit': 'GB/s', 'frac': lnamd_gbps / HBM_PEAK_GBPS,
+                                        'algorithmic_bytes': lnamd_bytes, 'avg_launch_ms': lnamd_avg_s * 1e3,
+                                        'note': 'stats + finalize + pool kernels timed together'}},
+        'cpu_baseline': None,
+    }
+    if not args.no_cpu_baseline:
+        log('[bench] timing the CPU baseline (oracle restatement, bounded sample)')
+        pools = pipeline.lnamd_pools(tokens, r_list)
+        scores = pipeline.msm_all(pools[:1, :1].contiguous())
+        torch.cuda.synchronize()
+        result['cpu_baseline'] = cpu_baseline(tokens_cpu, pools, r_list, image_size, scores[0, 0].cpu())
+        log('[bench] CPU baseline done')
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == '__main__':
+    sys.exit(main())

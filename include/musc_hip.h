@@ -1,0 +1,173 @@
+/*
+ * musc_hip.h -- C-ABI of libmusc_hip.so, the MI355X (gfx950) implementation of
+ * MuSc's data-parallel hot path: mutual scoring (MSM), LNAMD neighbourhood
+ * aggregation, the score-map epilogue and ViT block attention.
+ *
+ * Conventions shared by every entry point
+ *   - All array pointers are DEVICE pointers unless a parameter says "host".
+ *   - Every launch is asynchronous on the given hipStream_t (0 = null stream);
+ *     nothing synchronises the host.
+ *   - The caller owns every buffer, including the workspace; the library keeps
+ *     no device state between calls.  Calls on different streams with
+ *     different workspaces may overlap.
+ *   - Return value: 0 on success, a hipError_t value (1..999) when the HIP
+ *     runtime reports an error, or a library code >= 1000 for argument errors
+ *     (see MUSC_ERR_*).  musc_strerror() turns any of them into text.
+ *
+ * The reference (DylanMartinLSC/musc-gpu) reaches its kernels through a ctypes
+ * bridge to NVRTC and the CUDA driver (models/modules/_cuda_runtime.py:58-100):
+ * it compiles CUDA C strings at first use and launches raw CUfunctions with
+ * data_ptr()/int arguments on torch's current stream.  This header replaces
+ * that bridge with fixed, typed entry points; each one names the reference
+ * function whose contract it serves.
+ */
+#ifndef MUSC_HIP_H
+#define MUSC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* Error codes (library-defined, >= 1000).                                   */
+/* ------------------------------------------------------------------------ */
+#define MUSC_OK                 0
+#define MUSC_ERR_INVALID_ARG    1001  /* bad shape, rank window, null pointer */
+#define MUSC_ERR_WORKSPACE      1002  /* workspace smaller than required      */
+#define MUSC_ERR_UNSUPPORTED    1003  /* shape outside the implemented range  */
+
+/* Text for any return code of this library (never NULL). */
+const char* musc_strerror(int code);
+
+/* Library version, as MAJOR*10000 + MINOR*100 + PATCH. */
+int musc_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Mutual scoring module (MSM).                                              */
+/* ------------------------------------------------------------------------ */
+
+/* Workspace needed by musc_msm_scores_f32 / musc_msm_nearest_f32 for a pool of
+ * n images x p patches x c channels.  Writes the byte count to *out.
+ * Replaces the scratch tensors the reference allocates inside
+ * models/modules/_MSM_gpu.py:717-748. */
+int musc_msm_workspace_bytes(int n, int p, int c, size_t* out);
+
+/* Mutual scores of a pool.
+ *   z       (n, p, c) fp32, row-major, contiguous.
+ *   rank_lo, rank_hi   trimmed rank window [rank_lo, rank_hi) over the n-1
+ *           per-reference-image minima, 0 <= rank_lo < rank_hi <= n-1.
+ *           The reference call site uses topmin_min=0, topmin_max=0.3, i.e.
+ *           rank_lo = int((n-1)*0), rank_hi = int((n-1)*0.3).
+ *   scores  (n, p) float64 out: for patch q of image i, the mean of ascending
+ *           ranks [rank_lo, rank_hi) of { min_r ||z[i,q]-z[j,r]||_2 : j != i },
+ *           the mean rounded to fp32 and widened to float64.
+ * Same contract as the reference's scoring plugin
+ * models/modules/_MSM_gpu.py:701-830 and the original
+ * models/modules/_MSM.py:10-30,53-59 (called at models/musc.py:254). */
+int musc_msm_scores_f32(const float* z, int n, int p, int c,
+                        int rank_lo, int rank_hi, double* scores,
+                        void* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+
+/* Per-reference-image nearest distances, the intermediate of the scoring:
+ *   nearest (n*p, n) fp32 out, nearest[i*p+q][j] = min_r ||z[i,q]-z[j,r]||_2
+ *           for j != i, and +inf for j == i.
+ * Matches `torch.min(torch.cdist(...), -1)[0]` of models/modules/_MSM.py:16-17
+ * and the `nearest` tensor of models/modules/_MSM_gpu.py:717. */
+int musc_msm_nearest_f32(const float* z, int n, int p, int c, float* nearest,
+                         void* workspace, size_t workspace_bytes,
+                         hipStream_t stream);
+
+/* The three stages of musc_msm_scores_f32, for callers that time or overlap
+ * them separately (same arguments and workspace):
+ *   prepare      row norms ||z||^2 and the +inf fill of the minima buffer;
+ *   pair_minima  fp32-MFMA pairwise distances of every unordered patch pair of
+ *                different images, reduced along rows and columns into the
+ *                per-(patch, image) minima (the hot kernel);
+ *   rank         trimmed rank means of the minima into scores.
+ * prepare must precede pair_minima, which must precede rank, on one stream. */
+int musc_msm_prepare_f32(const float* z, int n, int p, int c,
+                         void* workspace, size_t workspace_bytes, hipStream_t stream);
+int musc_msm_pair_minima_f32(const float* z, int n, int p, int c,
+                             void* workspace, size_t workspace_bytes, hipStream_t stream);
+int musc_msm_rank_f32(int n, int p, int rank_lo, int rank_hi, double* scores,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* LNAMD: per-image LayerNorm over (C,H,W) + r x r zero-padded box mean.     */
+/* ------------------------------------------------------------------------ */
+#define MUSC_DTYPE_F32 0
+#define MUSC_DTYPE_F16 1
+
+/* Output layouts of musc_lnamd_f32 (R radii, L layers, B images, P patches). */
+#define MUSC_LAYOUT_RBPLC 0  /* out[r][b][p][l][c]: one (B,P,L,C) block per radius,
+                                the aggregation plugin's return layout           */
+#define MUSC_LAYOUT_RLBPC 1  /* out[r][l][b][p][c]: one contiguous (B,P,C) pool
+                                per (radius, layer), the MSM input layout        */
+
+/* Flags for musc_lnamd_f32. */
+#define MUSC_LNAMD_L2NORM 1  /* also divide every output patch by its L2 norm over C
+                                (models/musc.py:238, fused)                        */
+#define MUSC_LNAMD_STATS_READY 2  /* the workspace already holds the LayerNorm
+                                statistics of these same tokens from an earlier
+                                call (e.g. another radius): skip the stats pass.
+                                Serves the per-division reuse of
+                                models/modules/_aggregation_cache.py:15-58.     */
+
+int musc_lnamd_workspace_bytes(int batch, int n_layers, size_t* out);
+
+/* tokens   host array of n_layers device pointers, each (batch, tokens_per_image, c)
+ *          of dtype in_dtype, contiguous.  When has_cls != 0 token 0 of each image
+ *          is the class token and is skipped; the remaining tokens form a
+ *          side x side grid (side*side == tokens_per_image - has_cls).
+ * radii    host array of n_radii odd radii (1, 3, 5, ...; r <= side).
+ * eps      LayerNorm epsilon (torch default 1e-5).
+ * out      fp32, layout out_layout, batch*P*n_layers*c*n_radii floats.
+ * Semantics per radius r and layer l (models/modules/_LNAMD.py:72-129 and the
+ * identity used by models/modules/_encoder_gpu.py:14-42,
+ * models/modules/_aggregation_cache.py:15-58):
+ *   y = (x - mean) / sqrt(var + eps) over all C*H*W values of one image (biased var,
+ *       unit weight, zero bias), then out = avg_pool2d(y, r, stride 1, pad r//2,
+ *       count_include_pad=True); with MUSC_LNAMD_L2NORM, out /= ||out||_2 over C. */
+int musc_lnamd_f32(const void* const* tokens, int n_layers, int in_dtype,
+                   int batch, int tokens_per_image, int c, int has_cls,
+                   const int* radii, int n_radii, float eps, int flags,
+                   float* out, int out_layout,
+                   void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Epilogue: layer/radius averaging, bilinear upsampling, image scores.      */
+/* ------------------------------------------------------------------------ */
+
+/* scores    (n_radii, n_layers, n, side*side) float64 per-(radius, layer) MSM maps.
+ * maps      (n, out_size, out_size) float64 out: mean over layers, then over radii
+ *           (models/musc.py:259,263), upsampled bilinearly with align_corners=True
+ *           (models/musc.py:269-272).
+ * image_scores (n,) float64 out: max over each upsampled map (models/musc.py:288).
+ *           May be NULL.  maps may be NULL when only image_scores are wanted. */
+int musc_maps_f64(const double* scores, int n_radii, int n_layers, int n, int side,
+                  int out_size, double* maps, double* image_scores,
+                  hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* ViT block attention: out = softmax(q k^T * scale) v per (batch*head).      */
+/* ------------------------------------------------------------------------ */
+
+/* q, k, v, out  (bh, t, d) contiguous, dtype MUSC_DTYPE_F32 or MUSC_DTYPE_F16
+ *               (fp16 storage, fp32 softmax and accumulation).
+ * Replaces the bmm -> softmax -> bmm of nn.MultiheadAttention inside
+ * models/backbone/open_clip/transformer.py:232-234 and the fused softmax
+ * models/modules/_attention_gpu.py:41-81,115-146.  d must be 64. */
+int musc_attention_fwd(const void* q, const void* k, const void* v, void* out,
+                       int dtype, int bh, int t, int d, float scale,
+                       hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MUSC_HIP_H */

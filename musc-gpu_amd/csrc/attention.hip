@@ -1,0 +1,205 @@
+// ViT block attention for gfx950: out = softmax(q k^T * scale) v, one pass with
+// online softmax (the logits never reach HBM).
+//
+// Reference: nn.MultiheadAttention's math path inside
+// models/backbone/open_clip/transformer.py:232-234 (bmm, softmax, bmm) and the
+// fused row softmax of models/modules/_attention_gpu.py:41-81 (fp32 max/sum,
+// fp16 storage).
+//
+// Layout trick: each wave computes S^T = K Q^T on fp32 MFMA
+// (v_mfma_f32_32x32x2f32) so that a lane owns ONE query (lane % 32) and 16 of the
+// 32 keys of a block in registers.  The row max / sum of the online softmax are
+// then in-register reductions plus one cross-half exchange, the rescale of the
+// running output is a per-lane scalar, and the probabilities already sit in the
+// B-operand layout of the second product O^T += V^T P^T, so P never goes through
+// LDS.  K and V^T blocks of 32 keys are staged in LDS and shared by the 4 waves
+// (128 queries) of a workgroup.
+#include <hip/hip_fp16.h>
+
+#include "common.hpp"
+
+namespace musc {
+namespace attn {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int D = 64;
+constexpr int KB = 32;              // keys per block
+constexpr int QW = 32;              // queries per wave
+constexpr int WAVES = 4;
+constexpr int KPITCH = D + 4;       // K block row pitch (floats)
+constexpr int VPITCH = KB + 4;      // V^T block row pitch (floats)
+
+template <int kDtype>
+__device__ inline float4 ld4(const void* base, long long idx4) {
+  if (kDtype == MUSC_DTYPE_F32) return reinterpret_cast<const float4*>(base)[idx4];
+  const uint2 raw = reinterpret_cast<const uint2*>(base)[idx4];
+  const float2 a = __half22float2(*reinterpret_cast<const __half2*>(&raw.x));
+  const float2 b = __half22float2(*reinterpret_cast<const __half2*>(&raw.y));
+  return make_float4(a.x, a.y, b.x, b.y);
+}
+
+template <int kDtype>
+__device__ inline void st4(void* base, long long idx4, float4 v) {
+  if (kDtype == MUSC_DTYPE_F32) {
+    reinterpret_cast<float4*>(base)[idx4] = v;
+  } else {
+    __half2 lo = __floats2half2_rn(v.x, v.y), hi = __floats2half2_rn(v.z, v.w);
+    uint2 raw;
+    raw.x = *reinterpret_cast<uint32_t*>(&lo);
+    raw.y = *reinterpret_cast<uint32_t*>(&hi);
+    reinterpret_cast<uint2*>(base)[idx4] = raw;
+  }
+}
+
+template <int kDtype>
+__global__ __launch_bounds__(WAVES * kWave) void attn_fwd_kernel(const void* __restrict__ qg, const void* __restrict__ kg,
+                                                                 const void* __restrict__ vg, void* __restrict__ og,
+                                                                 int t, float scale_log2) {
+  __shared__ __attribute__((aligned(16))) float Ks[KB * KPITCH];
+  __shared__ __attribute__((aligned(16))) float Vt[D * VPITCH];
+
+  const int bh = blockIdx.y;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int lq = lane & 31, lh = lane >> 5;
+  const int q = blockIdx.x * (QW * WAVES) + wave * QW + lq;
+  const long long head4 = (long long)bh * t * (D / 4);
+
+  // This lane's query row, pre-scaled by scale*log2(e): qr[s][j] = q[8s + 4h + j].
+  float qr[8][4];
+  {
+    const bool ok = q < t;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      float4 v = ok ? ld4<kDtype>(qg, head4 + (long long)q * (D / 4) + 2 * s + lh) : make_float4(0.f, 0.f, 0.f, 0.f);
+      qr[s][0] = v.x * scale_log2;
+      qr[s][1] = v.y * scale_log2;
+      qr[s][2] = v.z * scale_log2;
+      qr[s][3] = v.w * scale_log2;
+    }
+  }
+
+  floatx16 o0, o1;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    o0[v] = 0.f;
+    o1[v] = 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+
+  const int nkb = (t + KB - 1) / KB;
+  for (int kb = 0; kb < nkb; ++kb) {
+    // stage K (row-major) and V^T for keys kb*KB .. +KB
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int idx = threadIdx.x + i * WAVES * kWave;  // 0..511
+      const int key = idx / (D / 4), d4 = (idx % (D / 4)) * 4;
+      const int gk = kb * KB + key;
+      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+      if (gk < t) {
+        kv = ld4<kDtype>(kg, head4 + (long long)gk * (D / 4) + d4 / 4);
+        vv = ld4<kDtype>(vg, head4 + (long long)gk * (D / 4) + d4 / 4);
+      }
+      *reinterpret_cast<float4*>(&Ks[key * KPITCH + d4]) = kv;
+      Vt[(d4 + 0) * VPITCH + key] = vv.x;
+      Vt[(d4 + 1) * VPITCH + key] = vv.y;
+      Vt[(d4 + 2) * VPITCH + key] = vv.z;
+      Vt[(d4 + 3) * VPITCH + key] = vv.w;
+    }
+    __syncthreads();
+
+    // S^T (keys x queries), already in log2 units
+    floatx16 s;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) s[v] = 0.f;
+    const float* krow = &Ks[lq * KPITCH + 4 * lh];
+#pragma unroll
+    for (int ss = 0; ss < 8; ++ss) {
+      const float4 a = *reinterpret_cast<const float4*>(krow + 8 * ss);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, qr[ss][0], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, qr[ss][1], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, qr[ss][2], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, qr[ss][3], s, 0, 0, 0);
+    }
+    // mask keys beyond t; register v holds key (v/4)*8 + 4h + v%4 of the block
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int key = kb * KB + (v >> 2) * 8 + lh * 4 + (v & 3);
+      if (key >= t) s[v] = -INFINITY;
+      bmax = fmaxf(bmax, s[v]);
+    }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+    const float mnew = fmaxf(m, bmax);
+    const float alpha = exp2f(m - mnew);  // 0 on the first block (m = -inf)
+    float psum = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      s[v] = exp2f(s[v] - mnew);
+      psum += s[v];
+    }
+    psum += __shfl_xor(psum, 32, kWave);
+    l = l * alpha + psum;
+    m = mnew;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      o0[v] *= alpha;
+      o1[v] *= alpha;
+    }
+    // O^T += V^T P^T ; step e uses key 8*(e/4) + 4h + e%4 = register e of s
+    const float* vrow0 = &Vt[lq * VPITCH + 4 * lh];
+    const float* vrow1 = &Vt[(32 + lq) * VPITCH + 4 * lh];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float4 a0 = *reinterpret_cast<const float4*>(vrow0 + 8 * j);
+      const float4 a1 = *reinterpret_cast<const float4*>(vrow1 + 8 * j);
+      o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.x, s[4 * j + 0], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.x, s[4 * j + 0], o1, 0, 0, 0);
+      o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.y, s[4 * j + 1], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.y, s[4 * j + 1], o1, 0, 0, 0);
+      o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.z, s[4 * j + 2], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.z, s[4 * j + 2], o1, 0, 0, 0);
+      o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.w, s[4 * j + 3], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.w, s[4 * j + 3], o1, 0, 0, 0);
+    }
+    __syncthreads();
+  }
+
+  if (q < t) {
+    const float inv = 1.f / l;
+    // register v of tile dt holds d = 32*dt + (v/4)*8 + 4h + v%4
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 a = make_float4(o0[4 * g] * inv, o0[4 * g + 1] * inv, o0[4 * g + 2] * inv, o0[4 * g + 3] * inv);
+      const float4 b = make_float4(o1[4 * g] * inv, o1[4 * g + 1] * inv, o1[4 * g + 2] * inv, o1[4 * g + 3] * inv);
+      st4<kDtype>(og, head4 + (long long)q * (D / 4) + (8 * g + 4 * lh) / 4, a);
+      st4<kDtype>(og, head4 + (long long)q * (D / 4) + (32 + 8 * g + 4 * lh) / 4, b);
+    }
+  }
+}
+
+}  // namespace attn
+}  // namespace musc
+
+using namespace musc;
+
+extern "C" int musc_attention_fwd(const void* q, const void* k, const void* v, void* out, int dtype, int bh, int t,
+                                  int d, float scale, hipStream_t stream) {
+  if (!q || !k || !v || !out || bh < 1 || t < 1) return MUSC_ERR_INVALID_ARG;
+  if (dtype != MUSC_DTYPE_F32 && dtype != MUSC_DTYPE_F16) return MUSC_ERR_INVALID_ARG;
+  if (d != attn::D) return MUSC_ERR_UNSUPPORTED;
+  const uintptr_t align = dtype == MUSC_DTYPE_F32 ? 16 : 8;
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
+       reinterpret_cast<uintptr_t>(out)) % align)
+    return MUSC_ERR_INVALID_ARG;
+  if (bh > 65535) return MUSC_ERR_UNSUPPORTED;
+  const float scale_log2 = scale * 1.4426950408889634f;
+  dim3 grid((t + attn::QW * attn::WAVES - 1) / (attn::QW * attn::WAVES), bh);
+  if (dtype == MUSC_DTYPE_F32)
+    hipLaunchKernelGGL(attn::attn_fwd_kernel<MUSC_DTYPE_F32>, grid, dim3(attn::WAVES * kWave), 0, stream, q, k, v, out,
+                       t, scale_log2);
+  else
+    hipLaunchKernelGGL(attn::attn_fwd_kernel<MUSC_DTYPE_F16>, grid, dim3(attn::WAVES * kWave), 0, stream, q, k, v, out,
+                       t, scale_log2);
+  return check_launch();
+}

@@ -1,0 +1,16 @@
+// Library-wide C entry points: error strings and version.
+#include "common.hpp"
+
+extern "C" const char* musc_strerror(int code) {
+  switch (code) {
+    case MUSC_OK: return "success";
+    case MUSC_ERR_INVALID_ARG: return "musc: invalid argument (shape, rank window, pointer or alignment)";
+    case MUSC_ERR_WORKSPACE: return "musc: workspace is missing or smaller than required";
+    case MUSC_ERR_UNSUPPORTED: return "musc: shape outside the implemented range";
+    default: break;
+  }
+  if (code > 0 && code < 1000) return hipGetErrorString(static_cast<hipError_t>(code));
+  return "musc: unknown error code";
+}
+
+extern "C" int musc_version(void) { return 100; }

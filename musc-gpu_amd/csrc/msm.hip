@@ -1,0 +1,449 @@
+// Mutual scoring module (MSM) for gfx950.
+//
+// Reference semantics (models/modules/_MSM.py:10-30,53-59): for every patch q of
+// image i, d(q, j) = min_r ||z[i,q] - z[j,r]||_2 for every other image j, then the
+// score is the mean of ascending ranks [a, b) of {d(q, j)}_{j != i}.
+//
+// MI355X design
+//   1. msm_norms_kernel      ||z_row||^2 for all n*p rows (one wave per row).
+//   2. fill                  per-(row, image) minima buffer := +inf bits.
+//   3. msm_pair_min_kernel   the whole pool is one (n*p) x (n*p) Gram matrix.  Only
+//                            the upper triangle of 128x128 tiles is computed, on
+//                            fp32 MFMA (v_mfma_f32_32x32x2f32), so each unordered
+//                            patch pair's dot product is formed once.  The epilogue
+//                            turns dots into squared distances
+//                            ||a||^2 + ||b||^2 - 2 a.b (clamped at 0, as
+//                            torch.cdist's matmul path does), masks same-image
+//                            pairs, and reduces the tile along BOTH rows and
+//                            columns, segmented by image, merging the partial
+//                            minima with unsigned atomicMin on the float bits
+//                            (non-negative floats order like their bit patterns).
+//                            The distance matrix never reaches HBM.
+//   4. msm_rank_kernel       one wave per patch: rank the n-1 minima, average the
+//                            square roots of ranks [a, b).
+#include "common.hpp"
+
+namespace musc {
+namespace msm {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 128;          // tile rows (query patches)
+constexpr int BN = 128;          // tile columns (reference patches)
+constexpr int BK = 32;           // K chunk (channels) per pipeline stage
+constexpr int PITCH = BK + 4;    // LDS row pitch in floats for staged operands
+constexpr int EPITCH = BN + 1;   // LDS row pitch of the epilogue distance tile
+constexpr int THREADS = 256;     // 4 waves, each owns a 64x64 sub-tile
+constexpr int BAND = 8;          // tile rows per band of the tile enumeration
+constexpr uint32_t kInfBits = 0x7f800000u;
+
+constexpr int kStageFloats = 2 * (BM + BN) * PITCH;       // double-buffered A and B
+constexpr int kEpiFloats = BM * EPITCH;
+constexpr int kSmemFloats = kStageFloats > kEpiFloats ? kStageFloats : kEpiFloats;
+
+// ---------------------------------------------------------------------------
+// Tile enumeration.  Tiles (I, J), I <= J < T, are numbered band by band (BAND
+// tile rows per band); inside a band the triangle (J < I0 + h) comes first,
+// then the rectangle in column-major order, so that the workgroups one XCD runs
+// at the same time share a few A and B panels.
+// ---------------------------------------------------------------------------
+__host__ __device__ inline long long band_prefix(long long s, long long T) {
+  // tiles in bands 0..s-1, all of which are full (BAND rows)
+  return 36LL * s + 8LL * (T - 8) * s - 32LL * s * (s - 1);
+}
+
+__host__ __device__ inline long long total_tiles(long long T) { return T * (T + 1) / 2; }
+
+__device__ inline int2 decode_tile(long long w, long long T) {
+  const long long nb = (T + BAND - 1) / BAND;
+  long long lo = 0, hi = nb - 1;  // largest s with band_prefix(s) <= w
+  while (lo < hi) {
+    long long mid = (lo + hi + 1) >> 1;
+    if (band_prefix(mid, T) <= w) lo = mid; else hi = mid - 1;
+  }
+  const long long s = lo;
+  const long long I0 = s * BAND;
+  const long long h = (T - I0) < BAND ? (T - I0) : BAND;
+  long long q = w - band_prefix(s, T);
+  const long long tri = h * (h + 1) / 2;
+  if (q < tri) {
+    long long jl = (long long)((sqrt(8.0 * (double)q + 1.0) - 1.0) * 0.5);
+    while ((jl + 1) * (jl + 2) / 2 <= q) ++jl;
+    while (jl * (jl + 1) / 2 > q) --jl;
+    const long long il = q - jl * (jl + 1) / 2;
+    return make_int2((int)(I0 + il), (int)(I0 + jl));
+  }
+  q -= tri;
+  return make_int2((int)(I0 + q % h), (int)(I0 + h + q / h));
+}
+
+// ---------------------------------------------------------------------------
+// Row norms.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void msm_norms_kernel(const float* __restrict__ z, int rows, int c,
+                                                        float* __restrict__ norms) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const long long row = (long long)blockIdx.x * (blockDim.x / kWave) + wave;
+  if (row >= rows) return;
+  const float* src = z + row * (long long)c;
+  double acc = 0.0;
+  if ((c & 3) == 0) {
+    const float4* s4 = reinterpret_cast<const float4*>(src);
+    for (int k = lane; k < c / 4; k += kWave) {
+      float4 v = s4[k];
+      acc += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+    }
+  } else {
+    for (int k = lane; k < c; k += kWave) acc += (double)src[k] * src[k];
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) norms[row] = (float)acc;
+}
+
+// ---------------------------------------------------------------------------
+// Pairwise minima on fp32 MFMA.
+// ---------------------------------------------------------------------------
+template <bool kVec4>
+__device__ inline void load_chunk(const float* __restrict__ z, int rows, int c, int row0, int k0,
+                                  float4 (&reg)[4]) {
+  const int t = threadIdx.x;
+  const int lrow = t / (BK / 4);
+  const int lk = (t % (BK / 4)) * 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = row0 + lrow + 32 * i;
+    const int k = k0 + lk;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (r < rows) {
+      const float* src = z + (long long)r * c + k;
+      if (kVec4) {
+        if (k < c) v = *reinterpret_cast<const float4*>(src);
+      } else {
+        if (k + 0 < c) v.x = src[0];
+        if (k + 1 < c) v.y = src[1];
+        if (k + 2 < c) v.z = src[2];
+        if (k + 3 < c) v.w = src[3];
+      }
+    }
+    reg[i] = v;
+  }
+}
+
+__device__ inline void store_chunk(float* __restrict__ dst, const float4 (&reg)[4]) {
+  const int t = threadIdx.x;
+  const int lrow = t / (BK / 4);
+  const int lk = (t % (BK / 4)) * 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    *reinterpret_cast<float4*>(dst + (lrow + 32 * i) * PITCH + lk) = reg[i];
+}
+
+template <bool kVec4>
+__global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
+    const float* __restrict__ z, const float* __restrict__ norms, uint32_t* __restrict__ minbits,
+    int rows, int n, int p, int c, int T, long long ntiles) {
+  __shared__ __attribute__((aligned(16))) float smem[kSmemFloats];
+  __shared__ float s_rnorm[BM], s_cnorm[BN];
+  __shared__ int s_rimg[BM], s_cimg[BN];
+
+  const long long w = xcd_logical_id(blockIdx.x, gridDim.x);
+  if (w >= ntiles) return;
+  const int2 tile = decode_tile(w, T);
+  const int row0 = tile.x * BM, col0 = tile.y * BN;
+
+  const int t = threadIdx.x;
+  if (t < BM) {
+    const int r = row0 + t;
+    s_rnorm[t] = r < rows ? norms[r] : 0.f;
+    s_rimg[t] = r < rows ? r / p : n;  // n marks "no image" (padding)
+  } else {
+    const int cc = col0 + (t - BM);
+    s_cnorm[t - BM] = cc < rows ? norms[cc] : 0.f;
+    s_cimg[t - BM] = cc < rows ? cc / p : n;
+  }
+
+  const int wave = t / kWave, lane = t % kWave;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lr = lane & 31, lh = lane >> 5;
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.f;
+
+  // Stage buffer `b` holds A rows at smem + b*(BM+BN)*PITCH, then B rows.
+  constexpr int kStage = (BM + BN) * PITCH;
+
+  float4 ra[4], rb[4];
+  const int nk = (c + BK - 1) / BK;
+  load_chunk<kVec4>(z, rows, c, row0, 0, ra);
+  load_chunk<kVec4>(z, rows, c, col0, 0, rb);
+  store_chunk(smem, ra);
+  store_chunk(smem + BM * PITCH, rb);
+  __syncthreads();
+
+  for (int kc = 0; kc < nk; ++kc) {
+    const int buf = kc & 1;
+    if (kc + 1 < nk) {
+      load_chunk<kVec4>(z, rows, c, row0, (kc + 1) * BK, ra);
+      load_chunk<kVec4>(z, rows, c, col0, (kc + 1) * BK, rb);
+    }
+    const float* A = smem + buf * kStage + (wm * 64 + lr) * PITCH + 4 * lh;
+    const float* B = smem + buf * kStage + BM * PITCH + (wn * 64 + lr) * PITCH + 4 * lh;
+#pragma unroll
+    for (int s = 0; s < BK / 8; ++s) {
+      const float4 a0 = *reinterpret_cast<const float4*>(A + 8 * s);
+      const float4 a1 = *reinterpret_cast<const float4*>(A + 32 * PITCH + 8 * s);
+      const float4 b0 = *reinterpret_cast<const float4*>(B + 8 * s);
+      const float4 b1 = *reinterpret_cast<const float4*>(B + 32 * PITCH + 8 * s);
+      const float av[2][4] = {{a0.x, a0.y, a0.z, a0.w}, {a1.x, a1.y, a1.z, a1.w}};
+      const float bv[2][4] = {{b0.x, b0.y, b0.z, b0.w}, {b1.x, b1.y, b1.z, b1.w}};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb)
+            acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[mb][e], bv[nb][e], acc[mb][nb], 0, 0, 0);
+    }
+    if (kc + 1 < nk) {
+      store_chunk(smem + (buf ^ 1) * kStage, ra);
+      store_chunk(smem + (buf ^ 1) * kStage + BM * PITCH, rb);
+    }
+    __syncthreads();
+  }
+
+  // Epilogue: squared distances into LDS (the operand buffers are free now).
+  float* E = smem;
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int j = wn * 64 + nb * 32 + lr;
+      const float cn = s_cnorm[j];
+      const int ci = s_cimg[j];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int i = wm * 64 + mb * 32 + (v >> 2) * 8 + lh * 4 + (v & 3);
+        float d2 = fmaf(-2.f, acc[mb][nb][v], s_rnorm[i] + cn);
+        d2 = fmaxf(d2, 0.f);
+        const int ri = s_rimg[i];
+        E[i * EPITCH + j] = (ri == ci || ri == n || ci == n) ? __int_as_float(kInfBits) : d2;
+      }
+    }
+  __syncthreads();
+
+  if (t < BM) {
+    // Row pass: minimum over this tile's columns, one segment per column image.
+    const int r = row0 + t;
+    if (r < rows) {
+      uint32_t* dst = minbits + (long long)r * n;
+      int seg = s_cimg[0];
+      float cur = __int_as_float(kInfBits);
+      for (int j = 0; j < BN; ++j) {
+        const int ci = s_cimg[j];
+        if (ci != seg) {
+          if (seg < n && cur < __int_as_float(kInfBits)) atomicMin(dst + seg, __float_as_uint(cur));
+          seg = ci;
+          cur = __int_as_float(kInfBits);
+        }
+        cur = fminf(cur, E[t * EPITCH + j]);
+      }
+      if (seg < n && cur < __int_as_float(kInfBits)) atomicMin(dst + seg, __float_as_uint(cur));
+    }
+  } else {
+    // Column pass: the same tile seen from the reference side (symmetric reuse).
+    const int j = t - BM;
+    const int cc = col0 + j;
+    if (cc < rows) {
+      uint32_t* dst = minbits + (long long)cc * n;
+      int seg = s_rimg[0];
+      float cur = __int_as_float(kInfBits);
+      for (int i = 0; i < BM; ++i) {
+        const int ri = s_rimg[i];
+        if (ri != seg) {
+          if (seg < n && cur < __int_as_float(kInfBits)) atomicMin(dst + seg, __float_as_uint(cur));
+          seg = ri;
+          cur = __int_as_float(kInfBits);
+        }
+        cur = fminf(cur, E[i * EPITCH + j]);
+      }
+      if (seg < n && cur < __int_as_float(kInfBits)) atomicMin(dst + seg, __float_as_uint(cur));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Trimmed rank mean.  One wave per query patch; the n minima are staged in LDS
+// and every value's rank is counted (ties broken by image index), so the sum of
+// ranks [a, b) is exact for any multiset.
+// ---------------------------------------------------------------------------
+constexpr int kRankWaves = 4;
+
+__global__ __launch_bounds__(kRankWaves * kWave) void msm_rank_kernel(
+    const uint32_t* __restrict__ minbits, int rows, int n, int p, int a, int b,
+    double* __restrict__ scores) {
+  extern __shared__ float s_vals[];  // kRankWaves * n
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const long long row = (long long)blockIdx.x * kRankWaves + wave;
+  float* vals = s_vals + wave * n;
+  const bool active = row < rows;
+  const int self = active ? (int)(row / p) : -1;
+  if (active) {
+    for (int j = lane; j < n; j += kWave)
+      vals[j] = j == self ? __int_as_float(kInfBits) : __uint_as_float(minbits[row * n + j]);
+  }
+  __syncthreads();
+  if (!active) return;
+  double sum = 0.0;
+  for (int j = lane; j < n; j += kWave) {
+    if (j == self) continue;
+    const float v = vals[j];
+    int rank = 0;
+    for (int k = 0; k < n; ++k) {
+      if (k == self) continue;
+      const float u = vals[k];
+      rank += (u < v) || (u == v && k < j);
+    }
+    if (rank >= a && rank < b) sum += (double)sqrtf(v);
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) scores[row] = (double)(float)(sum / (double)(b - a));
+}
+
+__global__ __launch_bounds__(256) void msm_nearest_kernel(const uint32_t* __restrict__ minbits,
+                                                          size_t count, int n, int p,
+                                                          float* __restrict__ nearest) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= count) return;
+  const size_t row = i / n;
+  const int j = (int)(i % n);
+  nearest[i] = (j == (int)(row / p)) ? __int_as_float(kInfBits) : sqrtf(__uint_as_float(minbits[i]));
+}
+
+struct Workspace {
+  float* norms;
+  uint32_t* minbits;
+};
+
+inline size_t workspace_bytes(long long n, long long p) {
+  const long long rows = n * p;
+  return align_up((size_t)rows * 4, 256) + align_up((size_t)rows * n * 4, 256);
+}
+
+inline Workspace carve(void* ws, long long n, long long p) {
+  const long long rows = n * p;
+  char* base = static_cast<char*>(ws);
+  Workspace w;
+  w.norms = reinterpret_cast<float*>(base);
+  w.minbits = reinterpret_cast<uint32_t*>(base + align_up((size_t)rows * 4, 256));
+  return w;
+}
+
+inline int validate(const float* z, int n, int p, int c, void* ws, size_t ws_bytes) {
+  if (!z || n < 2 || p < 1 || c < 1) return MUSC_ERR_INVALID_ARG;
+  const long long rows = (long long)n * p;
+  if (rows > (1LL << 30)) return MUSC_ERR_UNSUPPORTED;
+  if (n > 4096) return MUSC_ERR_UNSUPPORTED;  // rank kernel stages n floats per wave in LDS (64 KB)
+  if (!ws || ws_bytes < workspace_bytes(n, p)) return MUSC_ERR_WORKSPACE;
+  if ((c & 3) == 0 && (reinterpret_cast<uintptr_t>(z) & 15) != 0) return MUSC_ERR_INVALID_ARG;
+  return MUSC_OK;
+}
+
+// Stage 1: row norms and the +inf fill of the minima buffer.
+inline void run_prepare(const float* z, int n, int p, int c, const Workspace& w, hipStream_t s) {
+  const long long rows = (long long)n * p;
+  hipLaunchKernelGGL(msm_norms_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, z, (int)rows, c,
+                     w.norms);
+  launch_fill_u32(w.minbits, (size_t)rows * n, kInfBits, s);
+}
+
+// Stage 2: the fp32 MFMA pairwise-minima kernel (leaves squared minima bits).
+inline int run_pairs(const float* z, int n, int p, int c, const Workspace& w, hipStream_t s) {
+  const long long rows = (long long)n * p;
+  const long long T = (rows + BM - 1) / BM;
+  const long long ntiles = total_tiles(T);
+  const long long grid = (ntiles + kXcds - 1) / kXcds * kXcds;
+  if (grid > 0x7fffffffLL) return MUSC_ERR_UNSUPPORTED;
+  if ((c & 3) == 0)
+    hipLaunchKernelGGL(msm_pair_min_kernel<true>, dim3((unsigned)grid), dim3(THREADS), 0, s, z, w.norms,
+                       w.minbits, (int)rows, n, p, c, (int)T, ntiles);
+  else
+    hipLaunchKernelGGL(msm_pair_min_kernel<false>, dim3((unsigned)grid), dim3(THREADS), 0, s, z, w.norms,
+                       w.minbits, (int)rows, n, p, c, (int)T, ntiles);
+  return check_launch();
+}
+
+// Stage 3: trimmed rank means.
+inline int run_rank(int n, int p, int a, int b, double* scores, const Workspace& w, hipStream_t s) {
+  const long long rows = (long long)n * p;
+  const size_t smem = (size_t)kRankWaves * n * sizeof(float);
+  hipLaunchKernelGGL(msm_rank_kernel, dim3((unsigned)((rows + kRankWaves - 1) / kRankWaves)),
+                     dim3(kRankWaves * kWave), smem, s, w.minbits, (int)rows, n, p, a, b, scores);
+  return check_launch();
+}
+
+}  // namespace msm
+}  // namespace musc
+
+using namespace musc;
+
+extern "C" int musc_msm_workspace_bytes(int n, int p, int c, size_t* out) {
+  if (!out || n < 2 || p < 1 || c < 1) return MUSC_ERR_INVALID_ARG;
+  *out = msm::workspace_bytes(n, p);
+  return MUSC_OK;
+}
+
+extern "C" int musc_msm_prepare_f32(const float* z, int n, int p, int c, void* workspace, size_t workspace_bytes,
+                                    hipStream_t stream) {
+  int rc = msm::validate(z, n, p, c, workspace, workspace_bytes);
+  if (rc) return rc;
+  msm::run_prepare(z, n, p, c, msm::carve(workspace, n, p), stream);
+  return check_launch();
+}
+
+extern "C" int musc_msm_pair_minima_f32(const float* z, int n, int p, int c, void* workspace,
+                                        size_t workspace_bytes, hipStream_t stream) {
+  int rc = msm::validate(z, n, p, c, workspace, workspace_bytes);
+  if (rc) return rc;
+  return msm::run_pairs(z, n, p, c, msm::carve(workspace, n, p), stream);
+}
+
+extern "C" int musc_msm_rank_f32(int n, int p, int rank_lo, int rank_hi, double* scores, void* workspace,
+                                 size_t workspace_bytes, hipStream_t stream) {
+  if (!scores || n < 2 || p < 1 || rank_lo < 0 || rank_lo >= rank_hi || rank_hi > n - 1) return MUSC_ERR_INVALID_ARG;
+  if (n > 4096) return MUSC_ERR_UNSUPPORTED;
+  if (!workspace || workspace_bytes < msm::workspace_bytes(n, p)) return MUSC_ERR_WORKSPACE;
+  return msm::run_rank(n, p, rank_lo, rank_hi, scores, msm::carve(workspace, n, p), stream);
+}
+
+extern "C" int musc_msm_scores_f32(const float* z, int n, int p, int c, int rank_lo, int rank_hi,
+                                   double* scores, void* workspace, size_t workspace_bytes,
+                                   hipStream_t stream) {
+  int rc = msm::validate(z, n, p, c, workspace, workspace_bytes);
+  if (rc) return rc;
+  if (!scores || rank_lo < 0 || rank_lo >= rank_hi || rank_hi > n - 1) return MUSC_ERR_INVALID_ARG;
+  const msm::Workspace w = msm::carve(workspace, n, p);
+  msm::run_prepare(z, n, p, c, w, stream);
+  rc = msm::run_pairs(z, n, p, c, w, stream);
+  if (rc) return rc;
+  return msm::run_rank(n, p, rank_lo, rank_hi, scores, w, stream);
+}
+
+extern "C" int musc_msm_nearest_f32(const float* z, int n, int p, int c, float* nearest, void* workspace,
+                                    size_t workspace_bytes, hipStream_t stream) {
+  int rc = msm::validate(z, n, p, c, workspace, workspace_bytes);
+  if (rc) return rc;
+  if (!nearest) return MUSC_ERR_INVALID_ARG;
+  const msm::Workspace w = msm::carve(workspace, n, p);
+  msm::run_prepare(z, n, p, c, w, stream);
+  rc = msm::run_pairs(z, n, p, c, w, stream);
+  if (rc) return rc;
+  const size_t count = (size_t)n * p * n;
+  hipLaunchKernelGGL(msm::msm_nearest_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream,
+                     w.minbits, count, n, p, nearest);
+  return check_launch();
+}

@@ -1,0 +1,64 @@
+"""Build libmusc_hip.so for gfx950 from musc-gpu_amd/csrc/*.hip.
+
+    python musc-gpu_amd/musc_hip/build.py [-v]
+
+Every .hip file is compiled to its own object (in parallel), then linked into
+musc-gpu_amd/musc_hip/libmusc_hip.so.  The library is built in-tree so that it
+travels with the source tree to the GPU host.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import glob
+import os
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(ROOT, 'csrc')
+BUILD = os.path.join(ROOT, '_build')
+LIB = os.path.join(PKG, 'libmusc_hip.so')
+ARCH = os.environ.get('MUSC_OFFLOAD_ARCH', 'gfx950')
+HIPCC = os.environ.get('HIPCC', '/opt/rocm/bin/hipcc')
+
+# Packed FP32 instructions are disabled for all device code (they are emitted by
+# the compiler from ordinary float code otherwise).
+DEVICE_FLAGS = ['-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops']
+COMMON = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}', '-Wall', '-Wno-unused-function',
+          '-Wno-unused-variable', '-Wno-unused-but-set-variable'] + DEVICE_FLAGS
+
+
+def _compile(src: str, verbose: bool) -> str:
+    obj = os.path.join(BUILD, os.path.basename(src) + '.o')
+    cmd = [HIPCC] + COMMON + ['-c', src, '-o', obj]
+    if verbose:
+        print(' '.join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = 'packed-fp32-ops'
+    err = '\n'.join(line for line in res.stderr.splitlines() if noise not in line)
+    if res.returncode != 0:
+        raise RuntimeError(f'hipcc failed for {src}:\n{err}')
+    if err.strip() and verbose:
+        print(err, flush=True)
+    return obj
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    sources = sorted(glob.glob(os.path.join(CSRC, '*.hip')))
+    if not sources:
+        raise RuntimeError(f'no HIP sources under {CSRC}')
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose), sources))
+    tmp = LIB + '.tmp'
+    cmd = [HIPCC, '-shared', '-fPIC', f'--offload-arch={ARCH}', '-o', tmp] + objs
+    if verbose:
+        print(' '.join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == '__main__':
+    print(build(verbose='-v' in sys.argv))

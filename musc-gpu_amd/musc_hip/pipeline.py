@@ -1,0 +1,88 @@
+"""Fused scoring pipeline: layer tokens -> anomaly maps + image scores.
+
+Covers the hot path of MuSc.make_category_data (models/musc.py:225-288) for one
+division, starting from the encoder's layer tokens:
+
+    for r in r_list:                                   (musc.py:227)
+        features = LNAMD_r(tokens); features /= ||features||   (:235-238)
+        for l in layers: maps_l = MSM(Z_l, 0, 0.3)     (:250-256)
+        maps_r = mean_l maps_l                          (:259)
+    maps = mean_r maps_r; upsample bilinear align_corners  (:263-272)
+    image score = max(maps)                             (:288)
+
+MI355X layout: the whole pool stays resident in HBM.  One LNAMD launch reads
+every layer's tokens once and writes every (radius, layer) pool already
+L2-normalised and contiguous, (R, L, N, P, C) fp32 (5.6 GB at N=83, P=1369);
+the R*L MSM calls reuse one workspace and write into one (R, L, N, P) float64
+score tensor, which the epilogue kernel reduces, upsamples and maximises.
+Everything is asynchronous on torch's current stream.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _MSM_hip, _epilogue_hip, _lnamd_hip
+from . import _runtime as rt
+
+
+def lnamd_pools(tokens: list[torch.Tensor], r_list: list[int]) -> torch.Tensor:
+    """(R, L, N, P, C) fp32 L2-normalised LNAMD features (musc.py:227-243)."""
+    return _lnamd_hip.lnamd(tokens, r_list, l2norm=True, layout='rlbpc')
+
+
+def msm_all(pools: torch.Tensor, topmin_min: float = 0, topmin_max: float = 0.3,
+            pair_events: list | None = None) -> torch.Tensor:
+    """(R, L, N, P) float64 MSM maps of every (radius, layer) pool.
+
+    Runs the three MSM stages explicitly (prepare, pair minima, rank) so that a
+    caller can pass `pair_events`, a list that receives one (start, end)
+    torch.cuda.Event pair recorded around each pair-minima kernel on the stream
+    it runs on.
+    """
+    r, l, n, p, c = pools.shape
+    a, b = _MSM_hip.rank_window(n, topmin_min, topmin_max)
+    if not 0 <= a < b <= n - 1:
+        raise ValueError('Require valid nonempty trimmed ranks 0<=a<b<=N-1.')
+    if pools.dtype != torch.float32 or not pools.is_contiguous():
+        raise ValueError('pools must be a contiguous fp32 (R, L, N, P, C) tensor')
+    scores = torch.empty((r, l, n, p), dtype=torch.float64, device=pools.device)
+    ws = rt.workspace(_MSM_hip.workspace_bytes(n, p, c), pools.device)
+    lib = rt.library()
+    s = rt.stream(pools.device)
+    for ri in range(r):
+        for li in range(l):
+            z = pools[ri, li]
+            rt.check(lib.musc_msm_prepare_f32(z.data_ptr(), n, p, c, ws.data_ptr(), ws.numel(), s),
+                     'musc_msm_prepare_f32')
+            if pair_events is not None:
+                ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                ev[0].record()
+            rt.check(lib.musc_msm_pair_minima_f32(z.data_ptr(), n, p, c, ws.data_ptr(), ws.numel(), s),
+                     'musc_msm_pair_minima_f32')
+            if pair_events is not None:
+                ev[1].record()
+                pair_events.append(ev)
+            rt.check(lib.musc_msm_rank_f32(n, p, a, b, scores[ri, li].data_ptr(), ws.data_ptr(), ws.numel(), s),
+                     'musc_msm_rank_f32')
+    return scores
+
+
+def score_pool(tokens: list[torch.Tensor], r_list=(1, 3, 5), image_size: int = 518, topmin_min: float = 0,
+               topmin_max: float = 0.3, want_maps: bool = True, timing: dict | None = None):
+    """Tokens (list over layers of (N, 1+P, C) GPU tensors) -> (maps (N,1,S,S) f64, image scores (N,) f64).
+
+    `timing`, if given, receives torch.cuda.Event pairs: timing['lnamd'] (one
+    pair around the LNAMD launch) and timing['pairs'] (one per MSM pair kernel).
+    """
+    lnamd_ev = None
+    if timing is not None:
+        lnamd_ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        lnamd_ev[0].record()
+    pools = lnamd_pools(tokens, list(r_list))
+    if timing is not None:
+        lnamd_ev[1].record()
+        timing.setdefault('lnamd', []).append(lnamd_ev)
+    scores = msm_all(pools, topmin_min, topmin_max,
+                     pair_events=timing.setdefault('pairs', []) if timing is not None else None)
+    del pools
+    return _epilogue_hip.maps_and_scores(scores, image_size, want_maps=want_maps)

@@ -1,0 +1,41 @@
+"""Fused attention parity on the GPU vs torch softmax(q k^T * scale) v computed on the CPU."""
+import pytest
+import torch
+
+from musc_hip import _attention_hip
+
+pytestmark = pytest.mark.gpu
+
+
+def reference(q, k, v, scale):
+    q, k, v = (x.detach().cpu().float() for x in (q, k, v))
+    return torch.softmax((q * scale) @ k.transpose(1, 2), -1) @ v
+
+
+@pytest.mark.parametrize('bh,t', [(4, 1), (3, 33), (2, 77), (8, 1370)])
+def test_fp32(device, bh, t):
+    g = torch.Generator().manual_seed(bh * 10000 + t)
+    q, k, v = (torch.randn((bh, t, 64), generator=g) * 0.64 for _ in range(3))
+    out = _attention_hip.attention(q.to(device), k.to(device), v.to(device), 0.125).cpu()
+    ref = reference(q, k, v, 0.125)
+    torch.testing.assert_close(out, ref, rtol=1e-4, atol=2e-5)
+
+
+def test_fp16_storage(device):
+    g = torch.Generator().manual_seed(1)
+    q, k, v = (torch.randn((8, 1370, 64), generator=g).half() for _ in range(3))
+    out = _attention_hip.attention(q.to(device), k.to(device), v.to(device), 0.125).cpu()
+    assert out.dtype == torch.float16
+    ref = reference(q, k, v, 0.125)
+    torch.testing.assert_close(out.float(), ref, rtol=2e-3, atol=2e-3)
+
+
+def test_sharp_logits_select_one_row(device):
+    t = 100
+    q = torch.zeros((1, t, 64))
+    k = torch.zeros((1, t, 64))
+    q[0, :, 0] = 50.0
+    k[0, 37, 0] = 1.0
+    v = torch.randn((1, t, 64))
+    out = _attention_hip.attention(q.to(device), k.to(device), v.to(device), 1.0).cpu()
+    torch.testing.assert_close(out[0], v[0, 37].expand(t, 64), rtol=0, atol=1e-5)

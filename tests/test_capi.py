@@ -1,0 +1,97 @@
+"""The C-ABI library loads and exports what include/musc_hip.h declares (CPU only).
+
+Only argument-validation paths are called here: each returns its error code
+before any HIP call, so no GPU is touched.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, 'include', 'musc_hip.h')
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    return sorted(set(re.findall(r'\b(musc_\w+)\s*\(', text)))
+
+
+@pytest.fixture(scope='module')
+def lib():
+    from musc_hip import _runtime
+    return _runtime.library()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_functions()
+    assert 'musc_msm_scores_f32' in names and 'musc_lnamd_f32' in names
+    for name in names:
+        assert hasattr(lib, name), f'{name} declared in musc_hip.h but not exported'
+    from musc_hip import _runtime
+    assert set(names) == set(_runtime.SIGNATURES), 'ctypes signatures out of sync with the header'
+
+
+def test_version_and_strerror(lib):
+    assert lib.musc_version() >= 100
+    assert b'invalid argument' in lib.musc_strerror(1001)
+    assert b'workspace' in lib.musc_strerror(1002)
+    assert b'implemented range' in lib.musc_strerror(1003)
+    assert lib.musc_strerror(0) == b'success'
+
+
+def test_msm_workspace_bytes(lib):
+    out = ctypes.c_size_t()
+    assert lib.musc_msm_workspace_bytes(83, 1369, 1024, ctypes.byref(out)) == 0
+    rows = 83 * 1369
+    align = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    assert out.value == align(rows * 4) + align(rows * 83 * 4)
+    assert lib.musc_msm_workspace_bytes(1, 10, 10, ctypes.byref(out)) == 1001
+
+
+def test_msm_argument_errors_before_any_launch(lib):
+    fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    big = ctypes.c_size_t(1 << 40)
+    # empty rank window
+    assert lib.musc_msm_scores_f32(fake, 8, 10, 16, 2, 2, fake, fake, big, None) == 1001
+    # rank_hi beyond n-1
+    assert lib.musc_msm_scores_f32(fake, 8, 10, 16, 0, 8, fake, fake, big, None) == 1001
+    # n < 2
+    assert lib.musc_msm_scores_f32(fake, 1, 10, 16, 0, 1, fake, fake, big, None) == 1001
+    # workspace too small
+    assert lib.musc_msm_scores_f32(fake, 8, 10, 16, 0, 2, fake, fake, 16, None) == 1002
+    # null features
+    assert lib.musc_msm_scores_f32(None, 8, 10, 16, 0, 2, fake, fake, big, None) == 1001
+    # more images than the rank kernel stages
+    assert lib.musc_msm_scores_f32(fake, 5000, 1, 16, 0, 2, fake, fake, big, None) == 1003
+
+
+def test_lnamd_argument_errors(lib):
+    fake = ctypes.c_void_p(256)
+    ptrs = (ctypes.c_void_p * 1)(256)
+    radii = (ctypes.c_int * 1)(3)
+    even = (ctypes.c_int * 1)(2)
+    big = ctypes.c_size_t(1 << 40)
+    out = ctypes.c_size_t()
+    assert lib.musc_lnamd_workspace_bytes(4, 4, ctypes.byref(out)) == 0 and out.value > 0
+    # non-square grid
+    assert lib.musc_lnamd_f32(ptrs, 1, 0, 2, 27, 8, 1, radii, 1, 1e-5, 0, fake, 0, fake, big, None) == 1001
+    # even radius
+    assert lib.musc_lnamd_f32(ptrs, 1, 0, 2, 26, 8, 1, even, 1, 1e-5, 0, fake, 0, fake, big, None) == 1001
+    # channels not a multiple of 4
+    assert lib.musc_lnamd_f32(ptrs, 1, 0, 2, 26, 6, 1, radii, 1, 1e-5, 0, fake, 0, fake, big, None) == 1003
+    # unknown flag
+    assert lib.musc_lnamd_f32(ptrs, 1, 0, 2, 26, 8, 1, radii, 1, 1e-5, 8, fake, 0, fake, big, None) == 1001
+    # workspace too small
+    assert lib.musc_lnamd_f32(ptrs, 1, 0, 2, 26, 8, 1, radii, 1, 1e-5, 0, fake, 0, fake, 8, None) == 1002
+
+
+def test_maps_and_attention_argument_errors(lib):
+    fake = ctypes.c_void_p(256)
+    assert lib.musc_maps_f64(fake, 1, 1, 2, 5, 13, None, None, None) == 1001
+    assert lib.musc_maps_f64(fake, 1, 1, 2, 500, 13, fake, None, None) == 1003
+    assert lib.musc_attention_fwd(fake, fake, fake, fake, 0, 4, 10, 32, 0.125, None) == 1003
+    assert lib.musc_attention_fwd(fake, fake, fake, fake, 7, 4, 10, 64, 0.125, None) == 1001

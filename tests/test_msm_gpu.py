@@ -1,0 +1,119 @@
+"""MSM parity on the GPU: libmusc_hip vs the oracle (2e-5 absolute, the reference's gate)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import msm as om
+from musc_hip import _MSM_hip
+from musc_hip import synthetic
+
+pytestmark = pytest.mark.gpu
+ATOL = 2e-5  # tools/benchmark_support.py:11
+
+
+def _gpu(x, device):
+    return torch.as_tensor(x).to(device)
+
+
+@pytest.mark.parametrize('case', ['a', 'b', 'c', 'd'])
+def test_golden(golden, device, case):
+    g = golden('msm_small.npz')
+    z = _gpu(g[f'{case}_z'], device)
+    scores = _MSM_hip.MSM(z).cpu().numpy()
+    np.testing.assert_allclose(scores, g[f'{case}_scores'], rtol=0, atol=ATOL)
+    near = _MSM_hip.nearest(z).cpu().numpy()
+    np.testing.assert_allclose(near, g[f'{case}_nearest'], rtol=0, atol=ATOL)
+
+
+@pytest.mark.parametrize('n,p,c', [(5, 200, 36), (9, 130, 1024), (17, 64, 100), (6, 129, 7), (12, 257, 33),
+                                   (40, 3, 4)])
+def test_random_shapes_vs_oracles(device, n, p, c):
+    torch.manual_seed(n * 1000 + p)
+    z = torch.nn.functional.normalize(torch.randn((n, p, c)), dim=-1)
+    got = _MSM_hip.MSM(z.to(device)).cpu().numpy()
+    ref_t = om.MSM(z).numpy()
+    ref_64 = oracle.msm_scores_f64_c(z.numpy(), *om.rank_window(n))
+    np.testing.assert_allclose(got, ref_t, rtol=0, atol=ATOL)
+    np.testing.assert_allclose(got, ref_64, rtol=0, atol=ATOL)
+
+
+def test_rank_windows(device):
+    torch.manual_seed(3)
+    z = torch.randn((21, 50, 24))
+    for lo, hi in ((0.1, 0.5), (0, 1), (0.5, 0.2), (2, 5), (0, 20)):
+        got = _MSM_hip.MSM(z.to(device), topmin_min=lo, topmin_max=hi).cpu().numpy()
+        ref = om.MSM(z, lo, hi).numpy()
+        np.testing.assert_allclose(got, ref, rtol=0, atol=ATOL, err_msg=f'window {lo},{hi}')
+
+
+def test_nearest_vs_oracle(device):
+    torch.manual_seed(4)
+    z = torch.nn.functional.normalize(torch.randn((7, 300, 64)), dim=-1)
+    got = _MSM_hip.nearest(z.to(device)).cpu().numpy()
+    ref = om.nearest(z).numpy()
+    assert np.isinf(got[np.isinf(ref)]).all()
+    fin = np.isfinite(ref)
+    np.testing.assert_allclose(got[fin], ref[fin], rtol=0, atol=ATOL)
+
+
+def test_config1_plumbing_kernel_level(device):
+    # BASELINE config 1 shape: N=8, P=1369, C=1024, seeded N(0,1), L2-normalised
+    z = synthetic.msm_features(8, 1369, 1024, seed=42)
+    got = _MSM_hip.MSM(z.to(device)).cpu().numpy()
+    ref = om.MSM(z).numpy()
+    err = np.abs(got - ref).max()
+    print(f'config1 kernel-level max abs err {err:.3e}', flush=True)
+    assert err <= ATOL
+
+
+def test_default_pool_sampled_queries(device):
+    # BASELINE config 2 shape (N=83, P=1369, C=1024, correlated features); the oracle
+    # restates compute_scores_fast per query image, so three query images are checked.
+    toks = synthetic.pool_tokens(83, layers=1, seed=42)[0]
+    z = toks[:, 1:, :].contiguous()
+    got = _MSM_hip.MSM(z.to(device)).cpu().numpy()
+    for i in (0, 41, 82):
+        ref = om.compute_scores_fast(z, i).double().numpy()
+        err = np.abs(got[i] - ref).max()
+        print(f'config2 query image {i}: max abs err {err:.3e}', flush=True)
+        assert err <= ATOL
+
+
+def test_full_size_properties(device):
+    # BASELINE config 3 shape (N=83, P=784): deterministic, permutation-equivariant, scale-equivariant
+    z = synthetic.msm_features(83, 784, 1024, seed=7).to(device)
+    a = _MSM_hip.MSM(z)
+    b = _MSM_hip.MSM(z)
+    assert torch.equal(a, b), 'MSM must be bitwise deterministic'
+    perm = torch.randperm(83, generator=torch.Generator().manual_seed(1)).to(device)
+    c = _MSM_hip.MSM(z[perm].contiguous())
+    assert (c - a[perm]).abs().max().item() <= 1e-6
+    pp = torch.randperm(784, generator=torch.Generator().manual_seed(2)).to(device)
+    d = _MSM_hip.MSM(z[:, pp].contiguous())
+    assert (d - a[:, pp]).abs().max().item() <= 1e-6
+    e = _MSM_hip.MSM(z * 2.0)
+    assert (e - 2.0 * a).abs().max().item() <= 4e-6
+    # sampled oracle check of two query images at this shape
+    zc = z.cpu()
+    for i in (5, 77):
+        ref = om.compute_scores_fast(zc, i).double().numpy()
+        assert np.abs(a[i].cpu().numpy() - ref).max() <= ATOL
+
+
+def test_identical_images_score_near_zero(device):
+    base = torch.nn.functional.normalize(torch.randn((1, 64, 32)), dim=-1)
+    z = base.repeat(6, 1, 1).to(device)
+    got = _MSM_hip.MSM(z).cpu().numpy()
+    # exact answer 0; the expanded-norm form (like torch.cdist's matmul path) leaves
+    # at most sqrt of a few fp32 ulps of ||a||^2 + ||b||^2
+    assert got.max() < 1e-3
+
+
+def test_input_validation(device):
+    with pytest.raises(ValueError, match='nonempty trimmed ranks'):
+        _MSM_hip.MSM(torch.randn((4, 10, 8), device=device))
+    with pytest.raises(ValueError, match='CUDA FP32'):
+        _MSM_hip.MSM(torch.randn((8, 10, 8), device=device, dtype=torch.float64))
+    with pytest.raises(ValueError):
+        _MSM_hip.MSM(torch.randn((1, 10, 8), device=device))
