@@ -84,7 +84,7 @@ def cpu_baseline(tokens_cpu, pools_gpu, r_list, image_size, gpu_scores_rl0, budg
         if spent > budget_s and len(q_times) >= 2:
             break
     t_query = sum(q_times) / len(q_times)
-    fake = [[torch.rand((n, z.shape[0]), dtype=torch.float64) for _ in range(n_layers)] for _ in r_list]
+    fake = [[torch.rand((n, z.shape[1]), dtype=torch.float64) for _ in range(n_layers)] for _ in r_list]
     t2 = time.perf_counter()
     oe.maps_and_scores(fake, image_size)
     t_epi = time.perf_counter() - t2
