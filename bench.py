@@ -71,6 +71,7 @@ def cpu_baseline(tokens_cpu, pools_gpu, r_list, image_size, gpu_scores_rl0, budg
             ol.l2_normalise(f)
     t_lnamd_batch = time.perf_counter() - t0
     z = pools_gpu[0, 0].cpu()
+    z = z / z.norm(dim=-1, keepdim=True)      # the pools hold unnormalised window sums
     q_times, errs = [], []
     queries = [0, n // 2, n - 1, 1, n // 3, 2 * n // 3, n - 2, 5]
     spent = 0.0

@@ -82,15 +82,22 @@ int musc_msm_nearest_f32(const float* z, int n, int p, int c, float* nearest,
                          void* workspace, size_t workspace_bytes,
                          hipStream_t stream);
 
+/* Flags for musc_msm_prepare_f32. */
+#define MUSC_MSM_NORMALIZE_ROWS 1  /* score z_row / ||z_row|| instead of z_row: the L2
+                                      normalisation of models/musc.py:238 applied
+                                      inside MSM, so an aggregation that writes
+                                      unnormalised features needs no extra pass   */
+
 /* The three stages of musc_msm_scores_f32, for callers that time or overlap
  * them separately (same arguments and workspace):
- *   prepare      row norms ||z||^2 and the +inf fill of the minima buffer;
+ *   prepare      row norms ||z||^2 (and, with MUSC_MSM_NORMALIZE_ROWS, the row
+ *                scales 1/||z||) and the +inf fill of the minima buffer;
  *   pair_minima  fp32-MFMA pairwise distances of every unordered patch pair of
  *                different images, reduced along rows and columns into the
  *                per-(patch, image) minima (the hot kernel);
  *   rank         trimmed rank means of the minima into scores.
  * prepare must precede pair_minima, which must precede rank, on one stream. */
-int musc_msm_prepare_f32(const float* z, int n, int p, int c,
+int musc_msm_prepare_f32(const float* z, int n, int p, int c, int flags,
                          void* workspace, size_t workspace_bytes, hipStream_t stream);
 int musc_msm_pair_minima_f32(const float* z, int n, int p, int c,
                              void* workspace, size_t workspace_bytes, hipStream_t stream);
@@ -117,6 +124,11 @@ int musc_msm_rank_f32(int n, int p, int rank_lo, int rank_hi, double* scores,
                                 call (e.g. another radius): skip the stats pass.
                                 Serves the per-division reuse of
                                 models/modules/_aggregation_cache.py:15-58.     */
+#define MUSC_LNAMD_RAW_SUMS 4  /* write the r x r window sums of (x - mean) without
+                                the 1/sqrt(var+eps) and 1/r^2 factors: the input
+                                of an L2-normalising consumer (musc_msm_prepare_f32
+                                with MUSC_MSM_NORMALIZE_ROWS), for which those
+                                factors cancel.  Not combinable with L2NORM.     */
 
 int musc_lnamd_workspace_bytes(int batch, int n_layers, size_t* out);
 

@@ -129,13 +129,27 @@ __device__ inline float4 f4add(float4 a, float4 b) { return make_float4(a.x + b.
 __device__ inline float4 f4scale(float4 a, float s) { return make_float4(a.x * s, a.y * s, a.z * s, a.w * s); }
 __device__ inline float f4dot(float4 a) { return a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w; }
 
+// Sum of `v` over the 64 lanes of a wave, result in every lane: DPP within rows of
+// 16 lanes, then two cross-row exchanges.
+__device__ inline float wave_allsum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false));  // quad_perm 2,3,0,1
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xf, 0xf, false)); // row_half_mirror
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xf, 0xf, false)); // row_mirror
+  v += __shfl_xor(v, 16, kWave);
+  v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
 // grid: xcd-padded units * side; block = c/4 threads rounded up to a wave multiple.
-template <int kDtype, int kHalo, int kNR>
-__global__ __launch_bounds__(1024) void lnamd_pool_kernel(TokenPtrs tokens, int n_layers, int batch,
-                                                          int tokens_per_image, int c, int has_cls, int side,
-                                                          Radii radii, int l2norm, int layout,
-                                                          const double* __restrict__ stats,
-                                                          float* __restrict__ out, long long work) {
+// Radii arrive sorted ascending (the host keeps the caller's order in `slot`), so
+// the vertical sums nest: V_k = V_{k-1} + the rows between radius k-1 and k.
+template <int kDtype, int kHalo, int kNR, int kMaxThreads>
+__global__ __launch_bounds__(kMaxThreads) void lnamd_pool_kernel(TokenPtrs tokens, int n_layers, int batch,
+                                                                 int tokens_per_image, int c, int has_cls, int side,
+                                                                 Radii radii, Radii slot, int l2norm, int layout,
+                                                                 const double* __restrict__ stats,
+                                                                 float* __restrict__ out, long long work) {
   const long long wid = xcd_logical_id(blockIdx.x, gridDim.x);
   if (wid >= work) return;
   const int unit = (int)(wid / side), h = (int)(wid % side);
@@ -143,6 +157,7 @@ __global__ __launch_bounds__(1024) void lnamd_pool_kernel(TokenPtrs tokens, int 
   const int g = threadIdx.x;  // channel group (4 channels)
   const int groups = c / 4;
   const bool act = g < groups;
+  const int gl = act ? g : 0;  // inactive lanes read a valid address and discard it
   const void* base = tokens.p[l];
   const float mean = (float)stats[unit * 2 + 0];
   const float rstd = (float)stats[unit * 2 + 1];
@@ -153,72 +168,87 @@ __global__ __launch_bounds__(1024) void lnamd_pool_kernel(TokenPtrs tokens, int 
   const int nwaves = (blockDim.x + kWave - 1) / kWave;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
 
-  // vertical sums window: win[k][i] = V_{radius k}(column wo - kHalo + i)
+  // win[k][i]: vertical sum for radius k of column (current - kHalo + i), of x - mean
   float4 win[kNR][2 * kHalo + 1];
 #pragma unroll
   for (int k = 0; k < kNR; ++k)
 #pragma unroll
     for (int i = 0; i < 2 * kHalo + 1; ++i) win[k][i] = make_float4(0.f, 0.f, 0.f, 0.f);
 
-  // Shift the window left by one column and append the vertical sums of input
-  // column wi (zero outside the image).
-  auto push = [&](int wi) {
+  // Loads of input column wi, rows h-kHalo..h+kHalo; row and column validity are
+  // uniform over the workgroup, so out-of-image rows are skipped, not masked.
+  auto load_col = [&](int wi, float4 (&x)[2 * kHalo + 1]) {
+#pragma unroll
+    for (int dy = -kHalo; dy <= kHalo; ++dy) {
+      const int hh = h + dy;
+      if (wi < side && hh >= 0 && hh < side) {
+        const float4 r = load4<kDtype>(base, img_base4 + ((long long)(hh * side + wi) * c) / 4 + gl);
+        x[dy + kHalo] = make_float4(r.x - mean, r.y - mean, r.z - mean, r.w - mean);
+      } else {
+        x[dy + kHalo] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  };
+  auto push = [&](const float4 (&x)[2 * kHalo + 1]) {
 #pragma unroll
     for (int k = 0; k < kNR; ++k)
 #pragma unroll
       for (int i = 0; i < 2 * kHalo; ++i) win[k][i] = win[k][i + 1];
-    float4 vs[kNR];
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    int done = -1;  // rows |dy| <= done are in v
 #pragma unroll
-    for (int k = 0; k < kNR; ++k) vs[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (wi < side && act) {
+    for (int k = 0; k < kNR; ++k) {
+      const int hr = radii.r[k] / 2;
 #pragma unroll
-      for (int dy = -kHalo; dy <= kHalo; ++dy) {
-        const int hh = h + dy;
-        if (hh < 0 || hh >= side) continue;
-        float4 x = load4<kDtype>(base, img_base4 + ((long long)(hh * side + wi) * c) / 4 + g);
-        x = make_float4((x.x - mean) * rstd, (x.y - mean) * rstd, (x.z - mean) * rstd, (x.w - mean) * rstd);
-        const int ady = dy < 0 ? -dy : dy;
-#pragma unroll
-        for (int k = 0; k < kNR; ++k)
-          if (ady <= radii.r[k] / 2) vs[k] = f4add(vs[k], x);
+      for (int a = 0; a <= kHalo; ++a) {
+        if (a > done && a <= hr) {
+          v = f4add(v, x[kHalo + a]);
+          if (a > 0) v = f4add(v, x[kHalo - a]);
+        }
       }
+      done = hr > done ? hr : done;
+      win[k][2 * kHalo] = v;
     }
-#pragma unroll
-    for (int k = 0; k < kNR; ++k) win[k][2 * kHalo] = vs[k];
   };
 
+  {
+    float4 pre[kHalo > 0 ? kHalo : 1][2 * kHalo + 1];
 #pragma unroll
-  for (int wi = 0; wi < kHalo; ++wi) push(wi);
+    for (int wi = 0; wi < kHalo; ++wi) load_col(wi, pre[wi]);
+#pragma unroll
+    for (int wi = 0; wi < kHalo; ++wi) push(pre[wi]);
+  }
 
   for (int wb = 0; wb < side; wb += kColBatch) {
+    float4 xin[kColBatch][2 * kHalo + 1];
+#pragma unroll
+    for (int q = 0; q < kColBatch; ++q) load_col(wb + q + kHalo, xin[q]);
     float4 outs[kColBatch][kNR];
 #pragma unroll
     for (int q = 0; q < kColBatch; ++q) {
-      const int wo = wb + q;
-      push(wo + kHalo);
-      // horizontal sums for output column wo (window index kHalo is column wo)
+      push(xin[q]);
+      // horizontal sums for output column wb + q (window index kHalo)
 #pragma unroll
       for (int k = 0; k < kNR; ++k) {
         const int hr = radii.r[k] / 2;
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 acc = win[k][kHalo];
 #pragma unroll
-        for (int i = 0; i < 2 * kHalo + 1; ++i) {
-          const int dx = i - kHalo;
-          if ((dx < 0 ? -dx : dx) <= hr) acc = f4add(acc, win[k][i]);
-        }
-        // the sum of the r*r normalised values (zeros outside), divided by r*r
-        outs[q][k] = f4scale(acc, 1.f / (float)(radii.r[k] * radii.r[k]));
+        for (int a = 1; a <= kHalo; ++a)
+          if (a <= hr) acc = f4add(f4add(acc, win[k][kHalo - a]), win[k][kHalo + a]);
+        outs[q][k] = acc;
       }
     }
     const int nb = side - wb < kColBatch ? side - wb : kColBatch;
 
-    float norm[kColBatch][kNR];  // per-patch L2 norms when l2norm is set
+    float scale[kColBatch][kNR];
     if (l2norm) {
+      // the LayerNorm scale and the 1/r^2 of the box mean cancel in the L2
+      // normalisation: out = S / ||S|| with S the window sum of x - mean
 #pragma unroll
       for (int q = 0; q < kColBatch; ++q)
 #pragma unroll
         for (int k = 0; k < kNR; ++k) {
-          const float v = wave_sum(act && q < nb ? f4dot(outs[q][k]) : 0.f);
+          const float v = wave_allsum(act && q < nb ? f4dot(outs[q][k]) : 0.f);
           if (lane == 0) red[q * kNR + k][wave] = v;
         }
       __syncthreads();
@@ -228,9 +258,14 @@ __global__ __launch_bounds__(1024) void lnamd_pool_kernel(TokenPtrs tokens, int 
         for (int k = 0; k < kNR; ++k) {
           float tot = 0.f;
           for (int w = 0; w < nwaves; ++w) tot += red[q * kNR + k][w];
-          norm[q][k] = sqrtf(tot);
+          scale[q][k] = 1.f / sqrtf(tot);
         }
       __syncthreads();
+    } else {
+#pragma unroll
+      for (int q = 0; q < kColBatch; ++q)
+#pragma unroll
+        for (int k = 0; k < kNR; ++k) scale[q][k] = rstd / (float)(radii.r[k] * radii.r[k]);
     }
     if (act) {
 #pragma unroll
@@ -239,21 +274,145 @@ __global__ __launch_bounds__(1024) void lnamd_pool_kernel(TokenPtrs tokens, int 
           const int p = h * side + wb + q;
 #pragma unroll
           for (int k = 0; k < kNR; ++k) {
+            const int ko = slot.r[k];
             long long o;
             if (layout == MUSC_LAYOUT_RBPLC)
-              o = ((((long long)k * batch + b) * P + p) * n_layers + l) * c;
+              o = ((((long long)ko * batch + b) * P + p) * n_layers + l) * c;
             else
-              o = ((((long long)k * n_layers + l) * batch + b) * P + p) * c;
-            float4 v = outs[q][k];
-            if (l2norm) {
-              const float nrm = norm[q][k];
-              v = make_float4(v.x / nrm, v.y / nrm, v.z / nrm, v.w / nrm);
-            }
-            reinterpret_cast<float4*>(out + o)[g] = v;
+              o = ((((long long)ko * n_layers + l) * batch + b) * P + p) * c;
+            reinterpret_cast<float4*>(out + o)[g] = f4scale(outs[q][k], scale[q][k]);
           }
         }
       }
     }
+  }
+}
+
+// Streaming variant (no cross-channel reduction).  One workgroup per (image,
+// layer, slice of cg channel groups); thread (w, gl) owns column w and channels
+// 4*(slice*cg + gl) .. +3 and sweeps the rows top to bottom.  The last 2*kHalo+1
+// input rows of its column (x - mean) live in a register ring; the vertical sums
+// of each output row go to LDS (double-buffered by row parity, one barrier per
+// row) and each thread adds its horizontal neighbours' sums from there.  Every
+// input value is read from HBM once and every output written once.
+//   raw = 0: out = window sum * rstd / r^2   (avg_pool2d of the LayerNorm output)
+//   raw = 1: out = window sum of (x - mean)  (unscaled; for consumers that
+//            L2-normalise, where the scale cancels)
+template <int kDtype, int kHalo, int kNR>
+__global__ __launch_bounds__(1024) void lnamd_stream_kernel(TokenPtrs tokens, int n_layers, int batch,
+                                                            int tokens_per_image, int c, int has_cls, int side,
+                                                            int cg, int slices, Radii radii, Radii slot, int raw,
+                                                            int layout, const double* __restrict__ stats,
+                                                            float* __restrict__ out) {
+  extern __shared__ float4 vsum[];  // [2][kNR][side * cg]
+  const int unit = blockIdx.x / slices, slice = blockIdx.x % slices;
+  const int b = unit / n_layers, l = unit % n_layers;
+  const int w = threadIdx.x / cg, gl = threadIdx.x % cg;
+  const int groups = c / 4;
+  const int g = slice * cg + gl;
+  const bool act = w < side && g < groups;
+  const int wl = act ? w : 0, gg = act ? g : 0;  // inactive threads read a valid address
+  const void* base = tokens.p[l];
+  const float mean = (float)stats[unit * 2 + 0];
+  const float rstd = (float)stats[unit * 2 + 1];
+  const int P = side * side;
+  const int row_len = side * cg;
+  const long long col_base4 = (((long long)b * tokens_per_image + has_cls) * c) / 4 + (long long)wl * (c / 4) + gg;
+  const long long row_step4 = (long long)side * (c / 4);
+
+  float4 ring[2 * kHalo + 1];
+#pragma unroll
+  for (int i = 0; i < 2 * kHalo + 1; ++i) ring[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 next = load4<kDtype>(base, col_base4);
+
+  for (int hi = 0; hi < side + kHalo; ++hi) {
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (hi < side) {
+      x = make_float4(next.x - mean, next.y - mean, next.z - mean, next.w - mean);
+      if (hi + 1 < side) next = load4<kDtype>(base, col_base4 + (long long)(hi + 1) * row_step4);
+    }
+#pragma unroll
+    for (int i = 0; i < 2 * kHalo; ++i) ring[i] = ring[i + 1];
+    ring[2 * kHalo] = x;
+    const int h = hi - kHalo;
+    if (h < 0) continue;
+    // nested vertical sums of row h (ring index kHalo) for the ascending radii
+    float4* buf = vsum + (size_t)(h & 1) * kNR * row_len;
+    {
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      int done = -1;
+#pragma unroll
+      for (int k = 0; k < kNR; ++k) {
+        const int hr = radii.r[k] / 2;
+#pragma unroll
+        for (int a = 0; a <= kHalo; ++a) {
+          if (a > done && a <= hr) {
+            v = f4add(v, ring[kHalo + a]);
+            if (a > 0) v = f4add(v, ring[kHalo - a]);
+          }
+        }
+        done = hr > done ? hr : done;
+        buf[k * row_len + threadIdx.x] = v;
+      }
+    }
+    __syncthreads();
+    if (act) {
+      const int p = h * side + w;
+#pragma unroll
+      for (int k = 0; k < kNR; ++k) {
+        const int hr = radii.r[k] / 2;
+        float4 acc = buf[k * row_len + threadIdx.x];
+#pragma unroll
+        for (int a = 1; a <= kHalo; ++a) {
+          if (a <= hr) {
+            if (w - a >= 0) acc = f4add(acc, buf[k * row_len + threadIdx.x - a * cg]);
+            if (w + a < side) acc = f4add(acc, buf[k * row_len + threadIdx.x + a * cg]);
+          }
+        }
+        const float sc = raw ? 1.f : rstd / (float)(radii.r[k] * radii.r[k]);
+        const int ko = slot.r[k];
+        long long o;
+        if (layout == MUSC_LAYOUT_RBPLC)
+          o = ((((long long)ko * batch + b) * P + p) * n_layers + l) * c;
+        else
+          o = ((((long long)ko * n_layers + l) * batch + b) * P + p) * c;
+        reinterpret_cast<float4*>(out + o)[g] = f4scale(acc, sc);
+      }
+    }
+  }
+}
+
+template <int kDtype, int kHalo>
+int dispatch_stream_nr(int nr, dim3 grid, dim3 block, size_t smem, hipStream_t s, const TokenPtrs& tp, int n_layers,
+                       int batch, int tpi, int c, int has_cls, int side, int cg, int slices, const Radii& radii,
+                       const Radii& slot, int raw, int layout, const double* stats, float* out) {
+#define MUSC_STREAM_CASE(NR)                                                                                      \
+  case NR:                                                                                                        \
+    hipLaunchKernelGGL((lnamd_stream_kernel<kDtype, kHalo, NR>), grid, block, smem, s, tp, n_layers, batch, tpi, c, \
+                       has_cls, side, cg, slices, radii, slot, raw, layout, stats, out);                          \
+    break;
+  switch (nr) {
+    MUSC_STREAM_CASE(1)
+    MUSC_STREAM_CASE(2)
+    MUSC_STREAM_CASE(3)
+    MUSC_STREAM_CASE(4)
+    default: return MUSC_ERR_UNSUPPORTED;
+  }
+#undef MUSC_STREAM_CASE
+  return MUSC_OK;
+}
+
+template <int kDtype>
+int dispatch_stream(int halo, int nr, dim3 grid, dim3 block, size_t smem, hipStream_t s, const TokenPtrs& tp,
+                    int n_layers, int batch, int tpi, int c, int has_cls, int side, int cg, int slices,
+                    const Radii& radii, const Radii& slot, int raw, int layout, const double* stats, float* out) {
+  switch (halo) {
+    case 0: return dispatch_stream_nr<kDtype, 0>(nr, grid, block, smem, s, tp, n_layers, batch, tpi, c, has_cls, side, cg, slices, radii, slot, raw, layout, stats, out);
+    case 1: return dispatch_stream_nr<kDtype, 1>(nr, grid, block, smem, s, tp, n_layers, batch, tpi, c, has_cls, side, cg, slices, radii, slot, raw, layout, stats, out);
+    case 2: return dispatch_stream_nr<kDtype, 2>(nr, grid, block, smem, s, tp, n_layers, batch, tpi, c, has_cls, side, cg, slices, radii, slot, raw, layout, stats, out);
+    case 3: return dispatch_stream_nr<kDtype, 3>(nr, grid, block, smem, s, tp, n_layers, batch, tpi, c, has_cls, side, cg, slices, radii, slot, raw, layout, stats, out);
+    case 4: return dispatch_stream_nr<kDtype, 4>(nr, grid, block, smem, s, tp, n_layers, batch, tpi, c, has_cls, side, cg, slices, radii, slot, raw, layout, stats, out);
+    default: return MUSC_ERR_UNSUPPORTED;
   }
 }
 
@@ -264,21 +423,27 @@ inline size_t workspace_bytes(long long batch, long long n_layers) {
 
 template <int kDtype, int kHalo, int kNR>
 void launch_pool(dim3 grid, dim3 block, hipStream_t s, const TokenPtrs& tp, int n_layers, int batch, int tpi, int c,
-                 int has_cls, int side, const Radii& radii, int l2norm, int layout, const double* stats, float* out,
-                 long long work) {
-  hipLaunchKernelGGL((lnamd_pool_kernel<kDtype, kHalo, kNR>), grid, block, 0, s, tp, n_layers, batch, tpi, c, has_cls,
-                     side, radii, l2norm, layout, stats, out, work);
+                 int has_cls, int side, const Radii& radii, const Radii& slot, int l2norm, int layout,
+                 const double* stats, float* out, long long work) {
+  // up to 256 threads (C <= 1024): the register budget of 2 waves per SIMD holds the
+  // whole column window; wider C uses 1024-thread workgroups
+  if (block.x <= 256)
+    hipLaunchKernelGGL((lnamd_pool_kernel<kDtype, kHalo, kNR, 256>), grid, block, 0, s, tp, n_layers, batch, tpi, c,
+                       has_cls, side, radii, slot, l2norm, layout, stats, out, work);
+  else
+    hipLaunchKernelGGL((lnamd_pool_kernel<kDtype, kHalo, kNR, 1024>), grid, block, 0, s, tp, n_layers, batch, tpi, c,
+                       has_cls, side, radii, slot, l2norm, layout, stats, out, work);
 }
 
 template <int kDtype, int kHalo>
 int dispatch_nr(int nr, dim3 grid, dim3 block, hipStream_t s, const TokenPtrs& tp, int n_layers, int batch, int tpi,
-                int c, int has_cls, int side, const Radii& radii, int l2norm, int layout, const double* stats,
-                float* out, long long work) {
+                int c, int has_cls, int side, const Radii& radii, const Radii& slot, int l2norm, int layout,
+                const double* stats, float* out, long long work) {
   switch (nr) {
-    case 1: launch_pool<kDtype, kHalo, 1>(grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, l2norm, layout, stats, out, work); break;
-    case 2: launch_pool<kDtype, kHalo, 2>(grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, l2norm, layout, stats, out, work); break;
-    case 3: launch_pool<kDtype, kHalo, 3>(grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, l2norm, layout, stats, out, work); break;
-    case 4: launch_pool<kDtype, kHalo, 4>(grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, l2norm, layout, stats, out, work); break;
+    case 1: launch_pool<kDtype, kHalo, 1>(grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, slot, l2norm, layout, stats, out, work); break;
+    case 2: launch_pool<kDtype, kHalo, 2>(grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, slot, l2norm, layout, stats, out, work); break;
+    case 3: launch_pool<kDtype, kHalo, 3>(grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, slot, l2norm, layout, stats, out, work); break;
+    case 4: launch_pool<kDtype, kHalo, 4>(grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, slot, l2norm, layout, stats, out, work); break;
     default: return MUSC_ERR_UNSUPPORTED;
   }
   return MUSC_OK;
@@ -286,14 +451,14 @@ int dispatch_nr(int nr, dim3 grid, dim3 block, hipStream_t s, const TokenPtrs& t
 
 template <int kDtype>
 int dispatch_halo(int halo, int nr, dim3 grid, dim3 block, hipStream_t s, const TokenPtrs& tp, int n_layers,
-                  int batch, int tpi, int c, int has_cls, int side, const Radii& radii, int l2norm, int layout,
-                  const double* stats, float* out, long long work) {
+                  int batch, int tpi, int c, int has_cls, int side, const Radii& radii, const Radii& slot, int l2norm,
+                  int layout, const double* stats, float* out, long long work) {
   switch (halo) {
-    case 0: return dispatch_nr<kDtype, 0>(nr, grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, l2norm, layout, stats, out, work);
-    case 1: return dispatch_nr<kDtype, 1>(nr, grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, l2norm, layout, stats, out, work);
-    case 2: return dispatch_nr<kDtype, 2>(nr, grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, l2norm, layout, stats, out, work);
-    case 3: return dispatch_nr<kDtype, 3>(nr, grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, l2norm, layout, stats, out, work);
-    case 4: return dispatch_nr<kDtype, 4>(nr, grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, l2norm, layout, stats, out, work);
+    case 0: return dispatch_nr<kDtype, 0>(nr, grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, slot, l2norm, layout, stats, out, work);
+    case 1: return dispatch_nr<kDtype, 1>(nr, grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, slot, l2norm, layout, stats, out, work);
+    case 2: return dispatch_nr<kDtype, 2>(nr, grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, slot, l2norm, layout, stats, out, work);
+    case 3: return dispatch_nr<kDtype, 3>(nr, grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, slot, l2norm, layout, stats, out, work);
+    case 4: return dispatch_nr<kDtype, 4>(nr, grid, block, s, tp, n_layers, batch, tpi, c, has_cls, side, radii, slot, l2norm, layout, stats, out, work);
     default: return MUSC_ERR_UNSUPPORTED;
   }
 }
@@ -318,7 +483,8 @@ extern "C" int musc_lnamd_f32(const void* const* tokens, int n_layers, int in_dt
   if (has_cls != 0 && has_cls != 1) return MUSC_ERR_INVALID_ARG;
   if (in_dtype != MUSC_DTYPE_F32 && in_dtype != MUSC_DTYPE_F16) return MUSC_ERR_INVALID_ARG;
   if (out_layout != MUSC_LAYOUT_RBPLC && out_layout != MUSC_LAYOUT_RLBPC) return MUSC_ERR_INVALID_ARG;
-  if ((flags & ~(MUSC_LNAMD_L2NORM | MUSC_LNAMD_STATS_READY)) != 0) return MUSC_ERR_INVALID_ARG;
+  if ((flags & ~(MUSC_LNAMD_L2NORM | MUSC_LNAMD_STATS_READY | MUSC_LNAMD_RAW_SUMS)) != 0) return MUSC_ERR_INVALID_ARG;
+  if ((flags & MUSC_LNAMD_L2NORM) && (flags & MUSC_LNAMD_RAW_SUMS)) return MUSC_ERR_INVALID_ARG;
   if (n_layers > kMaxLayers || n_radii > kMaxRadii) return MUSC_ERR_UNSUPPORTED;
   if (c % 4 != 0 || c / 4 > 1024) return MUSC_ERR_UNSUPPORTED;
   const int grid_tokens = tokens_per_image - has_cls;
@@ -335,6 +501,15 @@ extern "C" int musc_lnamd_f32(const void* const* tokens, int n_layers, int in_dt
     rr.r[k] = r;
     if (r / 2 > halo) halo = r / 2;
   }
+  // sort radii ascending for the nested vertical sums; slot[k] is the output index
+  Radii slot{};
+  slot.n = n_radii;
+  for (int k = 0; k < n_radii; ++k) slot.r[k] = k;
+  for (int i = 1; i < n_radii; ++i)
+    for (int j = i; j > 0 && rr.r[j - 1] > rr.r[j]; --j) {
+      int tr = rr.r[j - 1]; rr.r[j - 1] = rr.r[j]; rr.r[j] = tr;
+      int ts = slot.r[j - 1]; slot.r[j - 1] = slot.r[j]; slot.r[j] = ts;
+    }
   TokenPtrs tp{};
   const size_t align = in_dtype == MUSC_DTYPE_F32 ? 16 : 8;
   for (int l = 0; l < n_layers; ++l) {
@@ -361,17 +536,43 @@ extern "C" int musc_lnamd_f32(const void* const* tokens, int n_layers, int in_dt
     hipLaunchKernelGGL(lnamd_finalize_kernel<MUSC_DTYPE_F16>, dim3((units + 255) / 256), dim3(256), 0, stream, tp,
                        n_layers, units, tokens_per_image, c, has_cls, eps, partials, stats);
   }
-  const long long work = (long long)units * side;
-  const long long grid = (work + kXcds - 1) / kXcds * kXcds;
-  const int threads = ((c / 4 + kWave - 1) / kWave) * kWave;
-  const int l2 = (flags & MUSC_LNAMD_L2NORM) ? 1 : 0;
   int rc;
-  if (in_dtype == MUSC_DTYPE_F32)
-    rc = dispatch_halo<MUSC_DTYPE_F32>(halo, n_radii, dim3((unsigned)grid), dim3(threads), stream, tp, n_layers, batch,
-                                       tokens_per_image, c, has_cls, side, rr, l2, out_layout, stats, out, work);
-  else
-    rc = dispatch_halo<MUSC_DTYPE_F16>(halo, n_radii, dim3((unsigned)grid), dim3(threads), stream, tp, n_layers, batch,
-                                       tokens_per_image, c, has_cls, side, rr, l2, out_layout, stats, out, work);
+  if (flags & MUSC_LNAMD_L2NORM) {
+    // fused L2 normalisation: one workgroup owns all channels of an output row
+    if (c / 4 > 1024) return MUSC_ERR_UNSUPPORTED;
+    const long long work = (long long)units * side;
+    const long long grid = (work + kXcds - 1) / kXcds * kXcds;
+    const int threads = ((c / 4 + kWave - 1) / kWave) * kWave;
+    if (in_dtype == MUSC_DTYPE_F32)
+      rc = dispatch_halo<MUSC_DTYPE_F32>(halo, n_radii, dim3((unsigned)grid), dim3(threads), stream, tp, n_layers,
+                                         batch, tokens_per_image, c, has_cls, side, rr, slot, 1, out_layout, stats,
+                                         out, work);
+    else
+      rc = dispatch_halo<MUSC_DTYPE_F16>(halo, n_radii, dim3((unsigned)grid), dim3(threads), stream, tp, n_layers,
+                                         batch, tokens_per_image, c, has_cls, side, rr, slot, 1, out_layout, stats,
+                                         out, work);
+  } else {
+    // streaming kernel: cg channel groups per workgroup, side*cg <= 1024 threads
+    const int groups = c / 4;
+    int cg = 1;
+    while (cg * 2 <= 16 && cg * 2 <= groups && side * cg * 2 <= 1024 &&
+           (size_t)2 * n_radii * side * cg * 2 * sizeof(float4) <= 64 * 1024)
+      cg *= 2;
+    const size_t smem = (size_t)2 * n_radii * side * cg * sizeof(float4);
+    if (side * cg > 1024 || smem > 64 * 1024) return MUSC_ERR_UNSUPPORTED;
+    const int slices = (groups + cg - 1) / cg;
+    const int threads = side * cg;
+    const int raw = (flags & MUSC_LNAMD_RAW_SUMS) ? 1 : 0;
+    const dim3 grid((unsigned)(units * slices));
+    if (in_dtype == MUSC_DTYPE_F32)
+      rc = dispatch_stream<MUSC_DTYPE_F32>(halo, n_radii, grid, dim3(threads), smem, stream, tp, n_layers, batch,
+                                           tokens_per_image, c, has_cls, side, cg, slices, rr, slot, raw,
+                                           out_layout, stats, out);
+    else
+      rc = dispatch_stream<MUSC_DTYPE_F16>(halo, n_radii, grid, dim3(threads), smem, stream, tp, n_layers, batch,
+                                           tokens_per_image, c, has_cls, side, cg, slices, rr, slot, raw,
+                                           out_layout, stats, out);
+  }
   if (rc) return rc;
   return check_launch();
 }

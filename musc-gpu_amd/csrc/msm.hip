@@ -80,8 +80,11 @@ __device__ inline int2 decode_tile(long long w, long long T) {
 // ---------------------------------------------------------------------------
 // Row norms.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void msm_norms_kernel(const float* __restrict__ z, int rows, int c,
-                                                        float* __restrict__ norms) {
+// norms[row] = ||z_row||^2 and inv[row] = 1.  With `normalize`, the row is
+// treated as z / ||z|| (the L2 normalisation of models/musc.py:238 applied on the
+// fly): inv[row] = 1 / ||z_row|| and norms[row] = ||z_row||^2 * inv^2.
+__global__ __launch_bounds__(256) void msm_norms_kernel(const float* __restrict__ z, int rows, int c, int normalize,
+                                                        float* __restrict__ norms, float* __restrict__ inv) {
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const long long row = (long long)blockIdx.x * (blockDim.x / kWave) + wave;
   if (row >= rows) return;
@@ -97,7 +100,16 @@ __global__ __launch_bounds__(256) void msm_norms_kernel(const float* __restrict_
     for (int k = lane; k < c; k += kWave) acc += (double)src[k] * src[k];
   }
   acc = wave_sum(acc);
-  if (lane == 0) norms[row] = (float)acc;
+  if (lane == 0) {
+    if (normalize) {
+      const double r = 1.0 / sqrt(acc);
+      inv[row] = (float)r;
+      norms[row] = (float)(acc * r * r);
+    } else {
+      inv[row] = 1.f;
+      norms[row] = (float)acc;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -109,6 +121,15 @@ __device__ inline void load_chunk(const float* __restrict__ z, int rows, int c, 
   const int t = threadIdx.x;
   const int lrow = t / (BK / 4);
   const int lk = (t % (BK / 4)) * 4;
+  if (kVec4 && (c % BK) == 0) {
+    // whole chunks: no channel mask; padded rows re-read the last row (masked later)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = min(row0 + lrow + 32 * i, rows - 1);
+      reg[i] = *reinterpret_cast<const float4*>(z + (long long)r * c + k0 + lk);
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = row0 + lrow + 32 * i;
@@ -140,25 +161,37 @@ __device__ inline void store_chunk(float* __restrict__ dst, const float4 (&reg)[
 
 template <bool kVec4>
 __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
-    const float* __restrict__ z, const float* __restrict__ norms, uint32_t* __restrict__ minbits,
-    int rows, int n, int p, int c, int T, long long ntiles) {
+    const float* __restrict__ z, const float* __restrict__ norms, const float* __restrict__ inv,
+    uint32_t* __restrict__ minbits, int rows, int n, int p, int c, int T, long long ntiles) {
   __shared__ __attribute__((aligned(16))) float smem[kSmemFloats];
-  __shared__ float s_rnorm[BM], s_cnorm[BN];
+  __shared__ __attribute__((aligned(16))) float s_rnorm[BM];
+  __shared__ __attribute__((aligned(16))) float s_cnorm[BN];
+  __shared__ __attribute__((aligned(16))) float s_rinv[BM];   // row scales (1 unless normalising)
+  __shared__ __attribute__((aligned(16))) float s_cinv[BN];
   __shared__ int s_rimg[BM], s_cimg[BN];
 
   const long long w = xcd_logical_id(blockIdx.x, gridDim.x);
   if (w >= ntiles) return;
   const int2 tile = decode_tile(w, T);
   const int row0 = tile.x * BM, col0 = tile.y * BN;
+  // A tile is "simple" when its rows lie in one image and its columns in one image
+  // (all valid): the epilogue then reduces in registers.  A simple tile whose row
+  // and column image coincide holds only same-image pairs and is skipped.
+  const int rlast = min(row0 + BM, rows) - 1, clast = min(col0 + BN, rows) - 1;
+  const int rimg0 = row0 / p, cimg0 = col0 / p;
+  const bool simple = (row0 + BM <= rows) && (col0 + BN <= rows) && (rlast / p == rimg0) && (clast / p == cimg0);
+  if (simple && rimg0 == cimg0) return;
 
   const int t = threadIdx.x;
   if (t < BM) {
     const int r = row0 + t;
     s_rnorm[t] = r < rows ? norms[r] : 0.f;
+    s_rinv[t] = r < rows ? inv[r] : 0.f;
     s_rimg[t] = r < rows ? r / p : n;  // n marks "no image" (padding)
   } else {
     const int cc = col0 + (t - BM);
     s_cnorm[t - BM] = cc < rows ? norms[cc] : 0.f;
+    s_cinv[t - BM] = cc < rows ? inv[cc] : 0.f;
     s_cimg[t - BM] = cc < rows ? cc / p : n;
   }
 
@@ -177,20 +210,23 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
   // Stage buffer `b` holds A rows at smem + b*(BM+BN)*PITCH, then B rows.
   constexpr int kStage = (BM + BN) * PITCH;
 
-  float4 ra[4], rb[4];
+  float4 ra0[4], rb0[4], ra1[4], rb1[4];
   const int nk = (c + BK - 1) / BK;
-  load_chunk<kVec4>(z, rows, c, row0, 0, ra);
-  load_chunk<kVec4>(z, rows, c, col0, 0, rb);
-  store_chunk(smem, ra);
-  store_chunk(smem + BM * PITCH, rb);
+  load_chunk<kVec4>(z, rows, c, row0, 0, ra0);
+  load_chunk<kVec4>(z, rows, c, col0, 0, rb0);
+  if (nk > 1) {
+    load_chunk<kVec4>(z, rows, c, row0, BK, ra1);
+    load_chunk<kVec4>(z, rows, c, col0, BK, rb1);
+  }
+  store_chunk(smem, ra0);
+  store_chunk(smem + BM * PITCH, rb0);
+  if (nk > 2) {
+    load_chunk<kVec4>(z, rows, c, row0, 2 * BK, ra0);
+    load_chunk<kVec4>(z, rows, c, col0, 2 * BK, rb0);
+  }
   __syncthreads();
 
-  for (int kc = 0; kc < nk; ++kc) {
-    const int buf = kc & 1;
-    if (kc + 1 < nk) {
-      load_chunk<kVec4>(z, rows, c, row0, (kc + 1) * BK, ra);
-      load_chunk<kVec4>(z, rows, c, col0, (kc + 1) * BK, rb);
-    }
+  auto compute = [&](int buf) {
     const float* A = smem + buf * kStage + (wm * 64 + lr) * PITCH + 4 * lh;
     const float* B = smem + buf * kStage + BM * PITCH + (wn * 64 + lr) * PITCH + 4 * lh;
 #pragma unroll
@@ -209,11 +245,106 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
           for (int nb = 0; nb < 2; ++nb)
             acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[mb][e], bv[nb][e], acc[mb][nb], 0, 0, 0);
     }
+  };
+  // chunk j lives in register set j % 2 from its load until its LDS store one
+  // iteration before it is consumed; loads run two compute phases ahead.
+  for (int kc = 0; kc < nk; kc += 2) {
+    compute(0);
     if (kc + 1 < nk) {
-      store_chunk(smem + (buf ^ 1) * kStage, ra);
-      store_chunk(smem + (buf ^ 1) * kStage + BM * PITCH, rb);
+      store_chunk(smem + kStage, ra1);
+      store_chunk(smem + kStage + BM * PITCH, rb1);
+      if (kc + 3 < nk) {
+        load_chunk<kVec4>(z, rows, c, row0, (kc + 3) * BK, ra1);
+        load_chunk<kVec4>(z, rows, c, col0, (kc + 3) * BK, rb1);
+      }
     }
     __syncthreads();
+    if (kc + 1 >= nk) break;
+    compute(1);
+    if (kc + 2 < nk) {
+      store_chunk(smem, ra0);
+      store_chunk(smem + BM * PITCH, rb0);
+      if (kc + 4 < nk) {
+        load_chunk<kVec4>(z, rows, c, row0, (kc + 4) * BK, ra0);
+        load_chunk<kVec4>(z, rows, c, col0, (kc + 4) * BK, rb0);
+      }
+    }
+    __syncthreads();
+  }
+
+  if (simple) {
+    // Register epilogue.  Lane (lr, lh) of wave (wm, wn) holds, for mb, nb in {0,1} and
+    // v in 0..15, the dot of tile row wm*64 + mb*32 + (v/4)*8 + lh*4 + v%4 with tile
+    // column wn*64 + nb*32 + lr.
+    float d2[2][2][16];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[wm * 64 + mb * 32 + g * 8 + lh * 4]);
+        const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[wm * 64 + mb * 32 + g * 8 + lh * 4]);
+        const float rv[4] = {rn.x, rn.y, rn.z, rn.w};
+        const float rs[4] = {-2.f * ri.x, -2.f * ri.y, -2.f * ri.z, -2.f * ri.w};
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          const float cn = s_cnorm[wn * 64 + nb * 32 + lr];
+          const float ci = s_cinv[wn * 64 + nb * 32 + lr];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            d2[mb][nb][g * 4 + e] = fmaxf(fmaf(rs[e] * ci, acc[mb][nb][g * 4 + e], rv[e] + cn), 0.f);
+        }
+      }
+    // column minima over this wave's 64 rows: in-lane, then across the two lane halves
+    float cmin[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      float m = d2[0][nb][0];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) m = fminf(m, d2[mb][nb][v]);
+      cmin[nb] = m;
+    }
+    {
+      // half lh keeps column block nb = lh and receives the other half's value for it
+      const float send = lh ? cmin[0] : cmin[1];
+      const float keep = lh ? cmin[1] : cmin[0];
+      cmin[0] = fminf(keep, __shfl_xor(send, 32, kWave));
+    }
+    // row minima over this wave's 64 columns: min over nb in-lane, then a transposing
+    // butterfly over the 32 lanes of each half (31 exchanges); lane lr ends with the
+    // minimum of value index k = lr, i.e. row (lr/16)*32 + ((lr%16)/4)*8 + lh*4 + lr%4.
+    float rv[32];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) rv[mb * 16 + v] = fminf(d2[mb][0][v], d2[mb][1][v]);
+#pragma unroll
+    for (int bit = 4; bit >= 0; --bit) {
+      const int half = 1 << bit;
+      const bool up = (lr >> bit) & 1;
+#pragma unroll
+      for (int q = 0; q < half; ++q) {
+        const float send = up ? rv[q] : rv[q + half];
+        const float keep = up ? rv[q + half] : rv[q];
+        rv[q] = fminf(keep, __shfl_xor(send, half, kWave));
+      }
+    }
+    __syncthreads();  // operand buffers are no longer read
+    float* s_cmin = smem;             // [2 (wm)][BN]
+    float* s_rmin = smem + 2 * BN;    // [2 (wn)][BM]
+    s_cmin[wm * BN + wn * 64 + lh * 32 + lr] = cmin[0];
+    s_rmin[wn * BM + wm * 64 + (lr >> 4) * 32 + ((lr & 15) >> 2) * 8 + lh * 4 + (lr & 3)] = rv[0];
+    __syncthreads();
+    if (t < BM) {
+      const float m = fminf(s_rmin[t], s_rmin[BM + t]);
+      atomicMin(minbits + (long long)(row0 + t) * n + cimg0, __float_as_uint(m));
+    } else {
+      const int j = t - BM;
+      const float m = fminf(s_cmin[j], s_cmin[BN + j]);
+      atomicMin(minbits + (long long)(col0 + j) * n + rimg0, __float_as_uint(m));
+    }
+    return;
   }
 
   // Epilogue: squared distances into LDS (the operand buffers are free now).
@@ -224,11 +355,12 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
     for (int nb = 0; nb < 2; ++nb) {
       const int j = wn * 64 + nb * 32 + lr;
       const float cn = s_cnorm[j];
+      const float cs = -2.f * s_cinv[j];
       const int ci = s_cimg[j];
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int i = wm * 64 + mb * 32 + (v >> 2) * 8 + lh * 4 + (v & 3);
-        float d2 = fmaf(-2.f, acc[mb][nb][v], s_rnorm[i] + cn);
+        float d2 = fmaf(cs * s_rinv[i], acc[mb][nb][v], s_rnorm[i] + cn);
         d2 = fmaxf(d2, 0.f);
         const int ri = s_rimg[i];
         E[i * EPITCH + j] = (ri == ci || ri == n || ci == n) ? __int_as_float(kInfBits) : d2;
@@ -326,12 +458,13 @@ __global__ __launch_bounds__(256) void msm_nearest_kernel(const uint32_t* __rest
 
 struct Workspace {
   float* norms;
+  float* inv;
   uint32_t* minbits;
 };
 
 inline size_t workspace_bytes(long long n, long long p) {
   const long long rows = n * p;
-  return align_up((size_t)rows * 4, 256) + align_up((size_t)rows * n * 4, 256);
+  return 2 * align_up((size_t)rows * 4, 256) + align_up((size_t)rows * n * 4, 256);
 }
 
 inline Workspace carve(void* ws, long long n, long long p) {
@@ -339,7 +472,8 @@ inline Workspace carve(void* ws, long long n, long long p) {
   char* base = static_cast<char*>(ws);
   Workspace w;
   w.norms = reinterpret_cast<float*>(base);
-  w.minbits = reinterpret_cast<uint32_t*>(base + align_up((size_t)rows * 4, 256));
+  w.inv = reinterpret_cast<float*>(base + align_up((size_t)rows * 4, 256));
+  w.minbits = reinterpret_cast<uint32_t*>(base + 2 * align_up((size_t)rows * 4, 256));
   return w;
 }
 
@@ -354,10 +488,10 @@ inline int validate(const float* z, int n, int p, int c, void* ws, size_t ws_byt
 }
 
 // Stage 1: row norms and the +inf fill of the minima buffer.
-inline void run_prepare(const float* z, int n, int p, int c, const Workspace& w, hipStream_t s) {
+inline void run_prepare(const float* z, int n, int p, int c, int normalize, const Workspace& w, hipStream_t s) {
   const long long rows = (long long)n * p;
   hipLaunchKernelGGL(msm_norms_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, z, (int)rows, c,
-                     w.norms);
+                     normalize, w.norms, w.inv);
   launch_fill_u32(w.minbits, (size_t)rows * n, kInfBits, s);
 }
 
@@ -370,10 +504,10 @@ inline int run_pairs(const float* z, int n, int p, int c, const Workspace& w, hi
   if (grid > 0x7fffffffLL) return MUSC_ERR_UNSUPPORTED;
   if ((c & 3) == 0)
     hipLaunchKernelGGL(msm_pair_min_kernel<true>, dim3((unsigned)grid), dim3(THREADS), 0, s, z, w.norms,
-                       w.minbits, (int)rows, n, p, c, (int)T, ntiles);
+                       w.inv, w.minbits, (int)rows, n, p, c, (int)T, ntiles);
   else
     hipLaunchKernelGGL(msm_pair_min_kernel<false>, dim3((unsigned)grid), dim3(THREADS), 0, s, z, w.norms,
-                       w.minbits, (int)rows, n, p, c, (int)T, ntiles);
+                       w.inv, w.minbits, (int)rows, n, p, c, (int)T, ntiles);
   return check_launch();
 }
 
@@ -397,11 +531,12 @@ extern "C" int musc_msm_workspace_bytes(int n, int p, int c, size_t* out) {
   return MUSC_OK;
 }
 
-extern "C" int musc_msm_prepare_f32(const float* z, int n, int p, int c, void* workspace, size_t workspace_bytes,
-                                    hipStream_t stream) {
+extern "C" int musc_msm_prepare_f32(const float* z, int n, int p, int c, int flags, void* workspace,
+                                    size_t workspace_bytes, hipStream_t stream) {
   int rc = msm::validate(z, n, p, c, workspace, workspace_bytes);
   if (rc) return rc;
-  msm::run_prepare(z, n, p, c, msm::carve(workspace, n, p), stream);
+  if (flags & ~MUSC_MSM_NORMALIZE_ROWS) return MUSC_ERR_INVALID_ARG;
+  msm::run_prepare(z, n, p, c, (flags & MUSC_MSM_NORMALIZE_ROWS) ? 1 : 0, msm::carve(workspace, n, p), stream);
   return check_launch();
 }
 
@@ -427,7 +562,7 @@ extern "C" int musc_msm_scores_f32(const float* z, int n, int p, int c, int rank
   if (rc) return rc;
   if (!scores || rank_lo < 0 || rank_lo >= rank_hi || rank_hi > n - 1) return MUSC_ERR_INVALID_ARG;
   const msm::Workspace w = msm::carve(workspace, n, p);
-  msm::run_prepare(z, n, p, c, w, stream);
+  msm::run_prepare(z, n, p, c, 0, w, stream);
   rc = msm::run_pairs(z, n, p, c, w, stream);
   if (rc) return rc;
   return msm::run_rank(n, p, rank_lo, rank_hi, scores, w, stream);
@@ -439,7 +574,7 @@ extern "C" int musc_msm_nearest_f32(const float* z, int n, int p, int c, float* 
   if (rc) return rc;
   if (!nearest) return MUSC_ERR_INVALID_ARG;
   const msm::Workspace w = msm::carve(workspace, n, p);
-  msm::run_prepare(z, n, p, c, w, stream);
+  msm::run_prepare(z, n, p, c, 0, w, stream);
   rc = msm::run_pairs(z, n, p, c, w, stream);
   if (rc) return rc;
   const size_t count = (size_t)n * p * n;

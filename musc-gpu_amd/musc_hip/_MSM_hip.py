@@ -44,8 +44,13 @@ def workspace_bytes(n: int, p: int, c: int) -> int:
 
 
 def MSM(Z: torch.Tensor, device=None, topmin_min: float = 0, topmin_max: float = 0.3,
-        workspace: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
-    """(N, P) float64 mutual scores.  `workspace` / `out` let a caller reuse buffers."""
+        workspace: torch.Tensor | None = None, out: torch.Tensor | None = None,
+        normalize_rows: bool = False) -> torch.Tensor:
+    """(N, P) float64 mutual scores.  `workspace` / `out` let a caller reuse buffers.
+
+    normalize_rows scores Z[i, q] / ||Z[i, q]|| instead of Z[i, q] (the L2
+    normalisation of models/musc.py:238, applied inside the kernels).
+    """
     n, p, c = _validate(Z)
     a, b = rank_window(n, topmin_min, topmin_max)
     if not 0 <= a < b <= n - 1:
@@ -61,9 +66,17 @@ def MSM(Z: torch.Tensor, device=None, topmin_min: float = 0, topmin_max: float =
             scores = out
         else:
             scores = torch.empty((n, p), dtype=torch.float64, device=z.device)
-        rc = lib.musc_msm_scores_f32(z.data_ptr(), n, p, c, a, b, scores.data_ptr(), ws.data_ptr(), ws.numel(),
-                                     rt.stream(z.device))
-        rt.check(rc, 'musc_msm_scores_f32')
+        s = rt.stream(z.device)
+        if not normalize_rows:
+            rc = lib.musc_msm_scores_f32(z.data_ptr(), n, p, c, a, b, scores.data_ptr(), ws.data_ptr(), ws.numel(), s)
+            rt.check(rc, 'musc_msm_scores_f32')
+            return scores
+        rt.check(lib.musc_msm_prepare_f32(z.data_ptr(), n, p, c, rt.MSM_NORMALIZE_ROWS, ws.data_ptr(), ws.numel(), s),
+                 'musc_msm_prepare_f32')
+        rt.check(lib.musc_msm_pair_minima_f32(z.data_ptr(), n, p, c, ws.data_ptr(), ws.numel(), s),
+                 'musc_msm_pair_minima_f32')
+        rt.check(lib.musc_msm_rank_f32(n, p, a, b, scores.data_ptr(), ws.data_ptr(), ws.numel(), s),
+                 'musc_msm_rank_f32')
         return scores
 
 

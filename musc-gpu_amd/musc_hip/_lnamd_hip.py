@@ -47,7 +47,7 @@ def _check_tokens(tokens: list[torch.Tensor]) -> tuple[int, int, int, torch.dtyp
 
 def lnamd(tokens: list[torch.Tensor], radii: list[int], *, l2norm: bool = False, layout: str = 'rbplc',
           has_cls: bool = True, eps: float = 1e-5, stats_workspace: torch.Tensor | None = None,
-          stats_ready: bool = False) -> torch.Tensor:
+          stats_ready: bool = False, raw_sums: bool = False) -> torch.Tensor:
     """LayerNorm over (C, H, W) + r x r zero-padded box mean for every radius.
 
     tokens  list of L tensors (B, T, C) (T = 1 + side*side when has_cls).
@@ -55,6 +55,8 @@ def lnamd(tokens: list[torch.Tensor], radii: list[int], *, l2norm: bool = False,
       layout 'rbplc' -> (R, B, P, L, C)  (each [r] is the plugin's (B, P, L, C) return)
       layout 'rlbpc' -> (R, L, B, P, C)  (each [r, l] is a contiguous MSM pool)
     l2norm   also divides every patch by its L2 norm (models/musc.py:238).
+    raw_sums writes the window sums of (x - mean) without the LayerNorm scale and
+             the 1/r^2 (the input of an L2-normalising consumer, where they cancel).
     stats_workspace / stats_ready  reuse LayerNorm statistics computed by an
              earlier call on the same tokens (another radius).
     """
@@ -76,7 +78,8 @@ def lnamd(tokens: list[torch.Tensor], radii: list[int], *, l2norm: bool = False,
             raise ValueError('stats workspace too small')
         ptrs = (ctypes.c_void_p * n_layers)(*[x.data_ptr() for x in toks])
         rad = (ctypes.c_int * len(radii))(*radii)
-        flags = (rt.LNAMD_L2NORM if l2norm else 0) | (rt.LNAMD_STATS_READY if stats_ready else 0)
+        flags = ((rt.LNAMD_L2NORM if l2norm else 0) | (rt.LNAMD_STATS_READY if stats_ready else 0)
+                 | (rt.LNAMD_RAW_SUMS if raw_sums else 0))
         rc = rt.library().musc_lnamd_f32(ctypes.cast(ptrs, ctypes.c_void_p), n_layers,
                                          rt.DTYPE_F32 if dtype == torch.float32 else rt.DTYPE_F16,
                                          b, t, c, int(has_cls), ctypes.cast(rad, ctypes.c_void_p), len(radii),

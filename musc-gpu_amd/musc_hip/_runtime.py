@@ -34,6 +34,8 @@ LAYOUT_RBPLC = 0
 LAYOUT_RLBPC = 1
 LNAMD_L2NORM = 1
 LNAMD_STATS_READY = 2
+LNAMD_RAW_SUMS = 4
+MSM_NORMALIZE_ROWS = 1
 
 # Every symbol include/musc_hip.h declares, with its ctypes signature.
 _vp, _i, _f, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
@@ -43,7 +45,7 @@ SIGNATURES = {
     'musc_msm_workspace_bytes': (_i, [_i, _i, _i, ctypes.POINTER(_sz)]),
     'musc_msm_scores_f32': (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
     'musc_msm_nearest_f32': (_i, [_vp, _i, _i, _i, _vp, _vp, _sz, _vp]),
-    'musc_msm_prepare_f32': (_i, [_vp, _i, _i, _i, _vp, _sz, _vp]),
+    'musc_msm_prepare_f32': (_i, [_vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     'musc_msm_pair_minima_f32': (_i, [_vp, _i, _i, _i, _vp, _sz, _vp]),
     'musc_msm_rank_f32': (_i, [_i, _i, _i, _i, _vp, _vp, _sz, _vp]),
     'musc_lnamd_workspace_bytes': (_i, [_i, _i, ctypes.POINTER(_sz)]),

@@ -1,0 +1,167 @@
+"""Per-kernel micro-benchmarks of libmusc_hip on one GPU (used for rocprofv3 runs).
+
+    python musc-gpu_amd/musc_hip/kernels_bench.py msm [--n 83 --p 1369 --c 1024 --iters 3]
+    python musc-gpu_amd/musc_hip/kernels_bench.py lnamd [--n 83 --layers 4 --iters 3]
+    python musc-gpu_amd/musc_hip/kernels_bench.py attention [--dtype fp32|fp16 --blocks 24]
+    python musc-gpu_amd/musc_hip/kernels_bench.py copy [--mib 1024 --iters 3]
+    python musc-gpu_amd/musc_hip/kernels_bench.py msm lnamd copy --iters 1   (several in one process)
+
+Each prints one JSON line with the average duration of the kernel(s) from HIP
+events and the derived rate against the MI355X peak.  `copy` is a plain
+device-to-device copy of known size, the calibration point for rocprofv3
+FETCH_SIZE / WRITE_SIZE counters.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+if os.path.dirname(HERE) not in sys.path:
+    sys.path.insert(0, os.path.dirname(HERE))
+
+import torch  # noqa: E402
+
+from musc_hip import _MSM_hip, _attention_hip, _lnamd_hip, synthetic  # noqa: E402
+from musc_hip import _runtime as rt  # noqa: E402
+
+FP32_MFMA_TFLOPS = 157.3
+FP16_MFMA_TFLOPS = 2500.0
+HBM_GBPS = 8000.0
+
+
+def _events():
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def bench_msm(args):
+    dev = torch.device('cuda:0')
+    n, p, c = args.n, args.p, args.c
+    z = synthetic.msm_features(n, p, c, seed=42).to(dev)
+    a, b = _MSM_hip.rank_window(n)
+    ws = rt.workspace(_MSM_hip.workspace_bytes(n, p, c), dev)
+    scores = torch.empty((n, p), dtype=torch.float64, device=dev)
+    lib, s = rt.library(), rt.stream(dev)
+    t = {'prepare': [], 'pairs': [], 'rank': []}
+    for it in range(args.iters + 1):
+        evs = [_events() for _ in range(3)]
+        evs[0][0].record()
+        rt.check(lib.musc_msm_prepare_f32(z.data_ptr(), n, p, c, 0, ws.data_ptr(), ws.numel(), s), 'prepare')
+        evs[0][1].record()
+        evs[1][0].record()
+        rt.check(lib.musc_msm_pair_minima_f32(z.data_ptr(), n, p, c, ws.data_ptr(), ws.numel(), s), 'pairs')
+        evs[1][1].record()
+        evs[2][0].record()
+        rt.check(lib.musc_msm_rank_f32(n, p, a, b, scores.data_ptr(), ws.data_ptr(), ws.numel(), s), 'rank')
+        evs[2][1].record()
+        torch.cuda.synchronize()
+        if it > 0:
+            for k, (e0, e1) in zip(t, evs):
+                t[k].append(e0.elapsed_time(e1))
+        print(f'[msm] iteration {it} done', file=sys.stderr, flush=True)
+    avg = {k: sum(v) / len(v) for k, v in t.items()}
+    flop = float(c) * p * p * n * (n - 1)
+    tf = flop / (avg['pairs'] / 1e3) / 1e12
+    return {'kernel': 'msm', 'n': n, 'p': p, 'c': c, 'avg_ms': avg, 'pair_flop': flop, 'pair_tflops': tf,
+            'pair_frac_fp32_mfma_peak': tf / FP32_MFMA_TFLOPS}
+
+
+def bench_lnamd(args):
+    """All layers x radii 1/3/5 in one launch: the pipeline's variant (raw window sums,
+    normalised inside MSM) and the fused-L2 variant."""
+    dev = torch.device('cuda:0')
+    toks = [t.to(dev) for t in synthetic.pool_tokens(args.n, args.layers, seed=42)]
+    radii = [1, 3, 5]
+    n, L, T, C = args.n, args.layers, 1370, 1024
+    nbytes = 4.0 * n * L * (T * C + len(radii) * (T - 1) * C)
+    res = {'kernel': 'lnamd', 'n': n, 'layers': L, 'radii': radii, 'algorithmic_bytes': nbytes}
+    for name, kw in (('raw_sums', dict(raw_sums=True)), ('fused_l2', dict(l2norm=True))):
+        ts = []
+        for it in range(args.iters + 1):
+            e0, e1 = _events()
+            e0.record()
+            out = _lnamd_hip.lnamd(toks, radii, layout='rlbpc', **kw)
+            e1.record()
+            torch.cuda.synchronize()
+            if it > 0:
+                ts.append(e0.elapsed_time(e1))
+            del out
+            print(f'[lnamd {name}] iteration {it} done', file=sys.stderr, flush=True)
+        ms = sum(ts) / len(ts)
+        gbps = nbytes / (ms / 1e3) / 1e9
+        res[name] = {'avg_ms': ms, 'gbps': gbps, 'frac_hbm_peak': gbps / HBM_GBPS}
+    return res
+
+
+def bench_attention(args):
+    dev = torch.device('cuda:0')
+    dtype = torch.float32 if args.dtype == 'fp32' else torch.float16
+    B, H, T, D = 4, 16, 1370, 64
+    g = torch.Generator().manual_seed(42)
+    blocks = []
+    for k in range(args.blocks):
+        # seeded on the CPU, projected on the GPU (input generation only)
+        y = torch.randn((B * T, 1024), generator=g).to(dev)
+        w = (torch.randn((1024, 3 * 1024), generator=g) * 0.02).to(dev)
+        qkv = (y @ w).reshape(B, T, 3, H, D).permute(2, 0, 3, 1, 4).reshape(3, B * H, T, D)
+        blocks.append(tuple(x.contiguous().to(dev, dtype) for x in qkv))
+    ts = []
+    for it in range(args.iters + 1):
+        e0, e1 = _events()
+        e0.record()
+        for q, k, v in blocks:
+            _attention_hip.attention(q, k, v, D ** -0.5)
+        e1.record()
+        torch.cuda.synchronize()
+        if it > 0:
+            ts.append(e0.elapsed_time(e1) / len(blocks))
+        print(f'[attention] iteration {it} done', file=sys.stderr, flush=True)
+    ms = sum(ts) / len(ts)
+    flop = 4.0 * B * H * T * T * D
+    tf = flop / (ms / 1e3) / 1e12
+    peak = FP32_MFMA_TFLOPS if dtype == torch.float32 else FP16_MFMA_TFLOPS
+    return {'kernel': 'attention', 'dtype': args.dtype, 'B': B, 'H': H, 'T': T, 'D': D, 'blocks': args.blocks,
+            'avg_ms_per_block': ms, 'flop_per_block': flop, 'tflops': tf, 'frac_mfma_peak': tf / peak,
+            'peak_tflops': peak}
+
+
+def bench_copy(args):
+    dev = torch.device('cuda:0')
+    n = args.mib * (1 << 20) // 4
+    src = torch.randn(n, device=dev)
+    dst = torch.empty_like(src)
+    ts = []
+    for it in range(args.iters + 1):
+        e0, e1 = _events()
+        e0.record()
+        dst.copy_(src)
+        e1.record()
+        torch.cuda.synchronize()
+        if it > 0:
+            ts.append(e0.elapsed_time(e1))
+    ms = sum(ts) / len(ts)
+    return {'kernel': 'copy', 'bytes_read': n * 4, 'bytes_written': n * 4, 'avg_ms': ms,
+            'gbps_read_plus_write': 2 * n * 4 / (ms / 1e3) / 1e9}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('kernels', nargs='+', choices=['msm', 'lnamd', 'attention', 'copy'])
+    ap.add_argument('--n', type=int, default=83)
+    ap.add_argument('--p', type=int, default=1369)
+    ap.add_argument('--c', type=int, default=1024)
+    ap.add_argument('--layers', type=int, default=4)
+    ap.add_argument('--dtype', choices=['fp32', 'fp16'], default='fp32')
+    ap.add_argument('--blocks', type=int, default=24)
+    ap.add_argument('--mib', type=int, default=1024)
+    ap.add_argument('--iters', type=int, default=3)
+    args = ap.parse_args()
+    table = {'msm': bench_msm, 'lnamd': bench_lnamd, 'attention': bench_attention, 'copy': bench_copy}
+    for name in args.kernels:
+        print(json.dumps(table[name](args)), flush=True)
+
+
+if __name__ == '__main__':
+    main()

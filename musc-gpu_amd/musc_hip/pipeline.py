@@ -11,11 +11,15 @@ division, starting from the encoder's layer tokens:
     image score = max(maps)                             (:288)
 
 MI355X layout: the whole pool stays resident in HBM.  One LNAMD launch reads
-every layer's tokens once and writes every (radius, layer) pool already
-L2-normalised and contiguous, (R, L, N, P, C) fp32 (5.6 GB at N=83, P=1369);
-the R*L MSM calls reuse one workspace and write into one (R, L, N, P) float64
-score tensor, which the epilogue kernel reduces, upsamples and maximises.
-Everything is asynchronous on torch's current stream.
+every layer's tokens once and writes every (radius, layer) pool contiguous,
+(R, L, N, P, C) fp32 (5.6 GB at N=83, P=1369), as window sums of (x - mean):
+the LayerNorm scale and the 1/r^2 of the box mean cancel in the L2
+normalisation, which the MSM applies to each row on the fly
+(MUSC_MSM_NORMALIZE_ROWS: its norms pass computes 1/||row|| and the pair
+kernel's epilogue scales each dot product), so no pass over the 5.6 GB exists
+just to normalise.  The R*L MSM calls reuse one workspace and write into one
+(R, L, N, P) float64 score tensor, which the epilogue kernel reduces, upsamples
+and maximises.  Everything is asynchronous on torch's current stream.
 """
 from __future__ import annotations
 
@@ -26,12 +30,16 @@ from . import _runtime as rt
 
 
 def lnamd_pools(tokens: list[torch.Tensor], r_list: list[int]) -> torch.Tensor:
-    """(R, L, N, P, C) fp32 L2-normalised LNAMD features (musc.py:227-243)."""
-    return _lnamd_hip.lnamd(tokens, r_list, l2norm=True, layout='rlbpc')
+    """(R, L, N, P, C) fp32 LNAMD window sums of (x - mean), to be scored with normalize_rows.
+
+    Scored with row normalisation these give exactly the features of musc.py:227-243
+    (LayerNorm, box mean, L2 normalisation), up to fp32 rounding.
+    """
+    return _lnamd_hip.lnamd(tokens, r_list, raw_sums=True, layout='rlbpc')
 
 
 def msm_all(pools: torch.Tensor, topmin_min: float = 0, topmin_max: float = 0.3,
-            pair_events: list | None = None) -> torch.Tensor:
+            pair_events: list | None = None, normalize_rows: bool = True) -> torch.Tensor:
     """(R, L, N, P) float64 MSM maps of every (radius, layer) pool.
 
     Runs the three MSM stages explicitly (prepare, pair minima, rank) so that a
@@ -49,10 +57,11 @@ def msm_all(pools: torch.Tensor, topmin_min: float = 0, topmin_max: float = 0.3,
     ws = rt.workspace(_MSM_hip.workspace_bytes(n, p, c), pools.device)
     lib = rt.library()
     s = rt.stream(pools.device)
+    flags = rt.MSM_NORMALIZE_ROWS if normalize_rows else 0
     for ri in range(r):
         for li in range(l):
             z = pools[ri, li]
-            rt.check(lib.musc_msm_prepare_f32(z.data_ptr(), n, p, c, ws.data_ptr(), ws.numel(), s),
+            rt.check(lib.musc_msm_prepare_f32(z.data_ptr(), n, p, c, flags, ws.data_ptr(), ws.numel(), s),
                      'musc_msm_prepare_f32')
             if pair_events is not None:
                 ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))

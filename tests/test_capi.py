@@ -48,7 +48,7 @@ def test_msm_workspace_bytes(lib):
     assert lib.musc_msm_workspace_bytes(83, 1369, 1024, ctypes.byref(out)) == 0
     rows = 83 * 1369
     align = lambda x: (x + 255) // 256 * 256  # noqa: E731
-    assert out.value == align(rows * 4) + align(rows * 83 * 4)
+    assert out.value == 2 * align(rows * 4) + align(rows * 83 * 4)
     assert lib.musc_msm_workspace_bytes(1, 10, 10, ctypes.byref(out)) == 1001
 
 

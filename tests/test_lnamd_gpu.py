@@ -77,3 +77,17 @@ def test_constant_image_gives_zero(device):
     toks = torch.full((1, 26, 8), 2.5, device=device)
     out = _lnamd_hip.lnamd([toks], [1, 3, 5])
     assert out.abs().max().item() == 0.0
+
+
+def test_raw_sums_normalise_to_the_reference_features(device):
+    # window sums of (x - mean): scaling by rstd / r^2 gives the plugin output, and
+    # L2-normalising gives the features of models/musc.py:238
+    g = torch.Generator().manual_seed(9)
+    feats = [torch.randn((3, 1370, 1024), generator=g) + 0.5 for _ in range(2)]
+    dev = [f.to(device) for f in feats]
+    raw = _lnamd_hip.lnamd(dev, [5, 1, 3], raw_sums=True, layout='rlbpc').cpu()
+    for k, r in enumerate((5, 1, 3)):
+        ref = ol.l2_normalise(ol.aggregate_direct(feats, r))
+        for l in range(2):
+            got = raw[k, l] / raw[k, l].norm(dim=-1, keepdim=True)
+            assert (got - ref[:, :, l]).abs().max().item() <= ATOL

@@ -117,3 +117,14 @@ def test_input_validation(device):
         _MSM_hip.MSM(torch.randn((8, 10, 8), device=device, dtype=torch.float64))
     with pytest.raises(ValueError):
         _MSM_hip.MSM(torch.randn((1, 10, 8), device=device))
+
+
+def test_normalize_rows_equals_normalised_input(device):
+    torch.manual_seed(12)
+    z = torch.randn((11, 150, 96)) * 3.0 + 0.7
+    got = _MSM_hip.MSM(z.to(device), normalize_rows=True).cpu().numpy()
+    ref = om.MSM(torch.nn.functional.normalize(z, dim=-1)).numpy()
+    np.testing.assert_allclose(got, ref, rtol=0, atol=ATOL)
+    # without the flag the scores are those of the raw rows
+    raw = _MSM_hip.MSM(z.to(device)).cpu().numpy()
+    np.testing.assert_allclose(raw, om.MSM(z).numpy(), rtol=0, atol=1e-4)
