@@ -151,6 +151,14 @@ int musc_lnamd_f32(const void* const* tokens, int n_layers, int in_dtype,
                    float* out, int out_layout,
                    void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Adaptive average pooling of patch grids, F.adaptive_avg_pool2d semantics:
+ *   in   (batch, side_in*side_in, ch) fp32, out (batch, side_out*side_out, ch) fp32.
+ * The super_fast aggregation pools the r=3 LNAMD grid 37x37 -> 28x28
+ * (models/modules/_super_fast.py:17-27); a (B, P, L, C) block is pooled as
+ * batch = B, ch = L*C, an (R, L, N, P, C) pool as batch = R*L*N, ch = C. */
+int musc_adaptive_pool_f32(const float* in, int batch, int side_in, int ch, int side_out,
+                           float* out, hipStream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Epilogue: layer/radius averaging, bilinear upsampling, image scores.      */
 /* ------------------------------------------------------------------------ */

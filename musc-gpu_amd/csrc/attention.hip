@@ -178,6 +178,138 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_kernel(const void* __r
   }
 }
 
+// fp16 storage on fp16 MFMA (v_mfma_f32_32x32x16_f16): same S^T = K Q^T layout as
+// the fp32 kernel, four MFMAs per 32-key block for S (K = d = 64) and two per
+// 32-wide d tile for O^T += V^T P^T, with P rounded to fp16 (the reference feeds
+// fp16 probabilities to its second bmm, models/modules/_attention_gpu.py:141-146).
+// The softmax statistics stay fp32.  For MFMA m, lane half h, element j the
+// reduction index is k = 16m + 8h + j in S and key 16m + 8(j/4) + 4h + j%4 in
+// P V, which is exactly where register 8m + j of the S^T tile holds that key.
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+constexpr int KP16 = D + 8;        // K block pitch (halves): 144 B rows
+constexpr int VP16 = KB + 4;       // V^T block pitch (halves): 72 B rows
+
+__global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Float16* __restrict__ qg,
+                                                                     const _Float16* __restrict__ kg,
+                                                                     const _Float16* __restrict__ vg,
+                                                                     _Float16* __restrict__ og, int t,
+                                                                     float scale_log2) {
+  __shared__ __attribute__((aligned(16))) _Float16 Ks[KB * KP16];
+  __shared__ __attribute__((aligned(16))) _Float16 Vt[D * VP16];
+
+  const int bh = blockIdx.y;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int lq = lane & 31, lh = lane >> 5;
+  const int q = blockIdx.x * (QW * WAVES) + wave * QW + lq;
+  const long long head = (long long)bh * t * D;
+
+  half8 qf[4];
+  {
+    const bool ok = q < t;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      half8 v = {};
+      if (ok) v = *reinterpret_cast<const half8*>(qg + head + (long long)q * D + 16 * m + 8 * lh);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = (_Float16)((float)v[j] * scale_log2);
+      qf[m] = v;
+    }
+  }
+
+  floatx16 o0, o1;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    o0[v] = 0.f;
+    o1[v] = 0.f;
+  }
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const int nkb = (t + KB - 1) / KB;
+  const int tid = threadIdx.x;
+  for (int kb = 0; kb < nkb; ++kb) {
+    {
+      // K: 32 keys x 64 d, 8 halves per thread
+      const int key = tid / 8, d8 = (tid % 8) * 8;
+      const int gk = kb * KB + key;
+      half8 kv = {};
+      if (gk < t) kv = *reinterpret_cast<const half8*>(kg + head + (long long)gk * D + d8);
+      *reinterpret_cast<half8*>(&Ks[key * KP16 + d8]) = kv;
+      // V^T: keys 2kp, 2kp+1 x d 4dg..4dg+3 per thread, written as key pairs
+      const int kp = tid / 16, dg = tid % 16;
+      const int gk0 = kb * KB + 2 * kp, gk1 = gk0 + 1;
+      half4 v0 = {}, v1 = {};
+      if (gk0 < t) v0 = *reinterpret_cast<const half4*>(vg + head + (long long)gk0 * D + 4 * dg);
+      if (gk1 < t) v1 = *reinterpret_cast<const half4*>(vg + head + (long long)gk1 * D + 4 * dg);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+        half2v pr = {v0[i], v1[i]};
+        *reinterpret_cast<half2v*>(&Vt[(4 * dg + i) * VP16 + 2 * kp]) = pr;
+      }
+    }
+    __syncthreads();
+
+    floatx16 s;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) s[v] = 0.f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const half8 a = *reinterpret_cast<const half8*>(&Ks[lq * KP16 + 16 * m + 8 * lh]);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[m], s, 0, 0, 0);
+    }
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int key = kb * KB + (v >> 2) * 8 + lh * 4 + (v & 3);
+      if (key >= t) s[v] = -INFINITY;
+      bmax = fmaxf(bmax, s[v]);
+    }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+    const float mnew = fmaxf(m_run, bmax);
+    const float alpha = exp2f(m_run - mnew);
+    float psum = 0.f;
+    half8 pf[2];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const float e = exp2f(s[v] - mnew);
+      psum += e;
+      pf[v >> 3][v & 7] = (_Float16)e;
+    }
+    psum += __shfl_xor(psum, 32, kWave);
+    l_run = l_run * alpha + psum;
+    m_run = mnew;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      o0[v] *= alpha;
+      o1[v] *= alpha;
+    }
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) {
+      const half4 a0l = *reinterpret_cast<const half4*>(&Vt[lq * VP16 + 16 * mm + 4 * lh]);
+      const half4 a0h = *reinterpret_cast<const half4*>(&Vt[lq * VP16 + 16 * mm + 8 + 4 * lh]);
+      const half4 a1l = *reinterpret_cast<const half4*>(&Vt[(32 + lq) * VP16 + 16 * mm + 4 * lh]);
+      const half4 a1h = *reinterpret_cast<const half4*>(&Vt[(32 + lq) * VP16 + 16 * mm + 8 + 4 * lh]);
+      const half8 a0 = {a0l[0], a0l[1], a0l[2], a0l[3], a0h[0], a0h[1], a0h[2], a0h[3]};
+      const half8 a1 = {a1l[0], a1l[1], a1l[2], a1l[3], a1h[0], a1h[1], a1h[2], a1h[3]};
+      o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, pf[mm], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, pf[mm], o1, 0, 0, 0);
+    }
+    __syncthreads();
+  }
+
+  if (q < t) {
+    const float inv = 1.f / l_run;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 a = make_float4(o0[4 * g] * inv, o0[4 * g + 1] * inv, o0[4 * g + 2] * inv, o0[4 * g + 3] * inv);
+      const float4 b = make_float4(o1[4 * g] * inv, o1[4 * g + 1] * inv, o1[4 * g + 2] * inv, o1[4 * g + 3] * inv);
+      st4<MUSC_DTYPE_F16>(og, (head + (long long)q * D + 8 * g + 4 * lh) / 4, a);
+      st4<MUSC_DTYPE_F16>(og, (head + (long long)q * D + 32 + 8 * g + 4 * lh) / 4, b);
+    }
+  }
+}
+
 }  // namespace attn
 }  // namespace musc
 
@@ -188,7 +320,7 @@ extern "C" int musc_attention_fwd(const void* q, const void* k, const void* v, v
   if (!q || !k || !v || !out || bh < 1 || t < 1) return MUSC_ERR_INVALID_ARG;
   if (dtype != MUSC_DTYPE_F32 && dtype != MUSC_DTYPE_F16) return MUSC_ERR_INVALID_ARG;
   if (d != attn::D) return MUSC_ERR_UNSUPPORTED;
-  const uintptr_t align = dtype == MUSC_DTYPE_F32 ? 16 : 8;
+  const uintptr_t align = 16;
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
        reinterpret_cast<uintptr_t>(out)) % align)
     return MUSC_ERR_INVALID_ARG;
@@ -199,7 +331,8 @@ extern "C" int musc_attention_fwd(const void* q, const void* k, const void* v, v
     hipLaunchKernelGGL(attn::attn_fwd_kernel<MUSC_DTYPE_F32>, grid, dim3(attn::WAVES * kWave), 0, stream, q, k, v, out,
                        t, scale_log2);
   else
-    hipLaunchKernelGGL(attn::attn_fwd_kernel<MUSC_DTYPE_F16>, grid, dim3(attn::WAVES * kWave), 0, stream, q, k, v, out,
-                       t, scale_log2);
+    hipLaunchKernelGGL(attn::attn_fwd_f16_kernel, grid, dim3(attn::WAVES * kWave), 0, stream,
+                       static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
+                       static_cast<const _Float16*>(v), static_cast<_Float16*>(out), t, scale_log2);
   return check_launch();
 }

@@ -416,6 +416,30 @@ int dispatch_stream(int halo, int nr, dim3 grid, dim3 block, size_t smem, hipStr
   }
 }
 
+// Adaptive average pooling of a side_in x side_in patch grid to side_out x
+// side_out (F.adaptive_avg_pool2d semantics: output cell i averages input rows
+// floor(i*in/out) .. ceil((i+1)*in/out)-1, likewise for columns), over
+// `batch` grids of shape (side_in^2, ch) -> (side_out^2, ch).  One thread per
+// output float4; the window is at most 3 x 3 for 37 -> 28.
+__global__ __launch_bounds__(256) void adaptive_pool_kernel(const float* __restrict__ in, int batch, int side_in,
+                                                            int ch4, int side_out, float* __restrict__ out) {
+  const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long per_img = (long long)side_out * side_out * ch4;
+  if (idx >= per_img * batch) return;
+  const int bimg = (int)(idx / per_img);
+  const long long rem = idx % per_img;
+  const int po = (int)(rem / ch4), g = (int)(rem % ch4);
+  const int oy = po / side_out, ox = po % side_out;
+  const int y0 = (oy * side_in) / side_out, y1 = ((oy + 1) * side_in + side_out - 1) / side_out;
+  const int x0 = (ox * side_in) / side_out, x1 = ((ox + 1) * side_in + side_out - 1) / side_out;
+  const float4* src = reinterpret_cast<const float4*>(in) + (long long)bimg * side_in * side_in * ch4 + g;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int y = y0; y < y1; ++y)
+    for (int x = x0; x < x1; ++x) acc = f4add(acc, src[(long long)(y * side_in + x) * ch4]);
+  const float cnt = (float)((y1 - y0) * (x1 - x0));
+  reinterpret_cast<float4*>(out)[idx] = make_float4(acc.x / cnt, acc.y / cnt, acc.z / cnt, acc.w / cnt);
+}
+
 inline size_t workspace_bytes(long long batch, long long n_layers) {
   const long long units = batch * n_layers;
   return align_up((size_t)units * kChunks * 2 * sizeof(double), 256) + align_up((size_t)units * 2 * sizeof(double), 256);
@@ -574,5 +598,17 @@ extern "C" int musc_lnamd_f32(const void* const* tokens, int n_layers, int in_dt
                                            out_layout, stats, out);
   }
   if (rc) return rc;
+  return check_launch();
+}
+
+extern "C" int musc_adaptive_pool_f32(const float* in, int batch, int side_in, int ch, int side_out, float* out,
+                                      hipStream_t stream) {
+  if (!in || !out || batch < 1 || side_in < 1 || side_out < 1 || ch < 4) return MUSC_ERR_INVALID_ARG;
+  if (ch % 4 != 0) return MUSC_ERR_UNSUPPORTED;
+  if (((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) != 0) return MUSC_ERR_INVALID_ARG;
+  const long long total = (long long)batch * side_out * side_out * (ch / 4);
+  if (total == 0) return MUSC_OK;
+  hipLaunchKernelGGL(lnamd::adaptive_pool_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, in,
+                     batch, side_in, ch / 4, side_out, out);
   return check_launch();
 }

@@ -25,7 +25,7 @@ from __future__ import annotations
 
 import torch
 
-from . import _MSM_hip, _epilogue_hip, _lnamd_hip
+from . import _MSM_hip, _epilogue_hip, _lnamd_hip, _super_fast
 from . import _runtime as rt
 
 
@@ -77,17 +77,24 @@ def msm_all(pools: torch.Tensor, topmin_min: float = 0, topmin_max: float = 0.3,
 
 
 def score_pool(tokens: list[torch.Tensor], r_list=(1, 3, 5), image_size: int = 518, topmin_min: float = 0,
-               topmin_max: float = 0.3, want_maps: bool = True, timing: dict | None = None):
+               topmin_max: float = 0.3, want_maps: bool = True, timing: dict | None = None,
+               pool_grid: int | None = None):
     """Tokens (list over layers of (N, 1+P, C) GPU tensors) -> (maps (N,1,S,S) f64, image scores (N,) f64).
 
     `timing`, if given, receives torch.cuda.Event pairs: timing['lnamd'] (one
     pair around the LNAMD launch) and timing['pairs'] (one per MSM pair kernel).
+    `pool_grid` (the super_fast profile: 28) adaptively pools every patch grid to
+    pool_grid x pool_grid before scoring (models/modules/_super_fast.py:17-27).
     """
     lnamd_ev = None
     if timing is not None:
         lnamd_ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
         lnamd_ev[0].record()
     pools = lnamd_pools(tokens, list(r_list))
+    if pool_grid is not None:
+        r, l, n, p, c = pools.shape
+        pooled = _super_fast.adaptive_pool(pools.view(r * l * n, p, c), pool_grid)
+        pools = pooled.view(r, l, n, pool_grid * pool_grid, c)
     if timing is not None:
         lnamd_ev[1].record()
         timing.setdefault('lnamd', []).append(lnamd_ev)
