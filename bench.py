@@ -47,6 +47,21 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def profiled_traffic(config: str):
+    """HBM bytes per msm_pair_min_kernel launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (copy-kernel calibrated), or None when no summary covers `config`."""
+    if config != 'pool':
+        return None
+    path = os.path.join(ROOT, 'profiles', 'msm_lnamd_hbm_traffic_config2.md')
+    try:
+        for line in open(path):
+            if line.startswith('traffic_bytes_per_launch msm_pair_min_kernel config2:'):
+                return float(line.split(':')[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(tokens_cpu, pools_gpu, r_list, image_size, gpu_scores_rl0, budget_s: float = 20.0):
     """Time the oracle (torch CPU restatement of the original backend) on a bounded sample.
 
@@ -183,13 +198,14 @@ def main() -> int:
                    'seed': args.seed},
         'roofline': {'bound': 'mfma', 'kernel': 'msm_pair_min_kernel',
                      'achieved': achieved_tflops, 'peak': FP32_MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
-                     'frac': achieved_tflops / FP32_MFMA_PEAK_TFLOPS, 'traffic': None,
+                     'frac': achieved_tflops / FP32_MFMA_PEAK_TFLOPS, 'traffic': profiled_traffic(args.config),
+                     'traffic_source': 'profiles/msm_lnamd_hbm_traffic_config2.md (rocprofv3 PMC, copy-calibrated)',
                      'flop_per_launch': flop_per_launch, 'avg_launch_ms': pair_avg_s * 1e3,
                      'launches': len(pair_ms)},
         'kernels': {'lnamd_all_radii': {'bound': 'hbm', 'achieved': lnamd_gbps, 'peak': HBM_PEAK_GBPS,
                                         'unit': 'GB/s', 'frac': lnamd_gbps / HBM_PEAK_GBPS,
                                         'algorithmic_bytes': lnamd_bytes, 'avg_launch_ms': lnamd_avg_s * 1e3,
-                                        'note': 'stats + finalize + pool kernels timed together'}},
+                                        'note': 'stats + finalize + stream kernels timed together'}},
         'cpu_baseline': None,
     }
     if not args.no_cpu_baseline:

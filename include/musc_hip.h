@@ -186,6 +186,14 @@ int musc_attention_fwd(const void* q, const void* k, const void* v, void* out,
                        int dtype, int bh, int t, int d, float scale,
                        hipStream_t stream);
 
+/* Head-averaged attention probabilities:
+ *   weights (batch, t, t) fp32 out, weights[b][i][j] = mean over heads h of
+ *   softmax_j(q[b*heads+h][i] . k[b*heads+h][j] * scale); q, k (batch*heads, t, d).
+ * Serves the one block whose weights the encoder reads (need_weights=True,
+ * models/backbone/open_clip/transformer.py:232-234,331-333).  d = 64, t <= 2048. */
+int musc_attention_weights(const void* q, const void* k, int dtype, int batch, int heads,
+                           int t, int d, float scale, float* weights, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -310,6 +310,80 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
   }
 }
 
+// Head-averaged attention probabilities, for the one block whose weights the
+// caller reads (models/backbone/open_clip/transformer.py:331-333, averaged by
+// nn.MultiheadAttention over heads).  One workgroup per (batch, query row); each
+// thread owns keys tid, tid + 256, ... and accumulates mean_h softmax_h there.
+constexpr int kWMaxKeysPerThread = 8;   // t <= 2048
+
+template <int kDtype>
+__global__ __launch_bounds__(256) void attn_weights_kernel(const void* __restrict__ qg, const void* __restrict__ kg,
+                                                           int heads, int t, float scale,
+                                                           float* __restrict__ weights) {
+  const int b = blockIdx.x / t, i = blockIdx.x % t;
+  const int tid = threadIdx.x;
+  __shared__ float qrow[D];
+  __shared__ float red[256 / kWave];
+  float acc[kWMaxKeysPerThread];
+#pragma unroll
+  for (int m = 0; m < kWMaxKeysPerThread; ++m) acc[m] = 0.f;
+  for (int h = 0; h < heads; ++h) {
+    const long long head4 = ((long long)(b * heads + h) * t) * (D / 4);
+    __syncthreads();
+    if (tid < D / 4) {
+      const float4 v = ld4<kDtype>(qg, head4 + (long long)i * (D / 4) + tid);
+      qrow[4 * tid + 0] = v.x * scale;
+      qrow[4 * tid + 1] = v.y * scale;
+      qrow[4 * tid + 2] = v.z * scale;
+      qrow[4 * tid + 3] = v.w * scale;
+    }
+    __syncthreads();
+    float lg[kWMaxKeysPerThread];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int m = 0; m < kWMaxKeysPerThread; ++m) {
+      const int j = tid + 256 * m;
+      float dot = -INFINITY;
+      if (j < t) {
+        dot = 0.f;
+#pragma unroll
+        for (int d4 = 0; d4 < D / 4; ++d4) {
+          const float4 kv = ld4<kDtype>(kg, head4 + (long long)j * (D / 4) + d4);
+          dot = fmaf(qrow[4 * d4 + 0], kv.x, dot);
+          dot = fmaf(qrow[4 * d4 + 1], kv.y, dot);
+          dot = fmaf(qrow[4 * d4 + 2], kv.z, dot);
+          dot = fmaf(qrow[4 * d4 + 3], kv.w, dot);
+        }
+      }
+      lg[m] = dot;
+      mx = fmaxf(mx, dot);
+    }
+    mx = wave_max(mx);
+    if (tid % kWave == 0) red[tid / kWave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float sum = 0.f;
+#pragma unroll
+    for (int m = 0; m < kWMaxKeysPerThread; ++m) {
+      lg[m] = (tid + 256 * m < t) ? expf(lg[m] - mx) : 0.f;
+      sum += lg[m];
+    }
+    sum = wave_sum(sum);
+    __syncthreads();
+    if (tid % kWave == 0) red[tid / kWave] = sum;
+    __syncthreads();
+    sum = red[0] + red[1] + red[2] + red[3];
+#pragma unroll
+    for (int m = 0; m < kWMaxKeysPerThread; ++m) acc[m] += lg[m] / sum;
+  }
+  float* dst = weights + ((long long)b * t + i) * t;
+#pragma unroll
+  for (int m = 0; m < kWMaxKeysPerThread; ++m) {
+    const int j = tid + 256 * m;
+    if (j < t) dst[j] = acc[m] / (float)heads;
+  }
+}
+
 }  // namespace attn
 }  // namespace musc
 
@@ -334,5 +408,22 @@ extern "C" int musc_attention_fwd(const void* q, const void* k, const void* v, v
     hipLaunchKernelGGL(attn::attn_fwd_f16_kernel, grid, dim3(attn::WAVES * kWave), 0, stream,
                        static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
                        static_cast<const _Float16*>(v), static_cast<_Float16*>(out), t, scale_log2);
+  return check_launch();
+}
+
+extern "C" int musc_attention_weights(const void* q, const void* k, int dtype, int batch, int heads, int t, int d,
+                                      float scale, float* weights, hipStream_t stream) {
+  if (!q || !k || !weights || batch < 1 || heads < 1 || t < 1) return MUSC_ERR_INVALID_ARG;
+  if (dtype != MUSC_DTYPE_F32 && dtype != MUSC_DTYPE_F16) return MUSC_ERR_INVALID_ARG;
+  if (d != attn::D || t > 256 * attn::kWMaxKeysPerThread) return MUSC_ERR_UNSUPPORTED;
+  if (((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k)) % 16) != 0) return MUSC_ERR_INVALID_ARG;
+  const long long rows = (long long)batch * t;
+  if (rows > 0x7fffffffLL) return MUSC_ERR_UNSUPPORTED;
+  if (dtype == MUSC_DTYPE_F32)
+    hipLaunchKernelGGL(attn::attn_weights_kernel<MUSC_DTYPE_F32>, dim3((unsigned)rows), dim3(256), 0, stream, q, k,
+                       heads, t, scale, weights);
+  else
+    hipLaunchKernelGGL(attn::attn_weights_kernel<MUSC_DTYPE_F16>, dim3((unsigned)rows), dim3(256), 0, stream, q, k,
+                       heads, t, scale, weights);
   return check_launch();
 }

@@ -28,3 +28,23 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float) -
                                              bh, t, d, float(scale), rt.stream(q.device))
         rt.check(rc, 'musc_attention_fwd')
     return out
+
+
+def attention_weights(q: torch.Tensor, k: torch.Tensor, heads: int, scale: float) -> torch.Tensor:
+    """Head-averaged softmax(q k^T * scale): (B*H, T, 64) q, k -> (B, T, T) fp32."""
+    for name, x in (('q', q), ('k', k)):
+        rt.require_device_tensor(x, name)
+    if q.shape != k.shape or q.ndim != 3 or q.dtype != k.dtype or q.dtype not in (torch.float32, torch.float16):
+        raise ValueError('q and k must share one (B*H, T, D) float32/float16 shape')
+    bh, t, d = q.shape
+    if bh % heads:
+        raise ValueError('leading dimension must be batch * heads')
+    q, k = q.contiguous(), k.contiguous()
+    with torch.cuda.device(q.device):
+        out = torch.empty((bh // heads, t, t), dtype=torch.float32, device=q.device)
+        rc = rt.library().musc_attention_weights(q.data_ptr(), k.data_ptr(),
+                                                 rt.DTYPE_F32 if q.dtype == torch.float32 else rt.DTYPE_F16,
+                                                 bh // heads, heads, t, d, float(scale), out.data_ptr(),
+                                                 rt.stream(q.device))
+        rt.check(rc, 'musc_attention_weights')
+    return out

@@ -53,6 +53,7 @@ SIGNATURES = {
     'musc_maps_f64': (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp]),
     'musc_adaptive_pool_f32': (_i, [_vp, _i, _i, _i, _i, _vp, _vp]),
     'musc_attention_fwd': (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp]),
+    'musc_attention_weights': (_i, [_vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _vp]),
 }
 
 _lock = threading.Lock()
