@@ -173,6 +173,17 @@ int musc_maps_f64(const double* scores, int n_radii, int n_layers, int n, int si
                   int out_size, double* maps, double* image_scores,
                   hipStream_t stream);
 
+/* RsCIN refinement of image scores (models/modules/_RsCIN.py:5-32):
+ *   cls_tokens   (n, d) fp32 L2-normalised class tokens (models/musc.py:215,218);
+ *   image_scores (n,) float64 raw image scores (map maxima, models/musc.py:288);
+ *   k_list       host array of n_k neighbourhood sizes (1 <= k <= n; MVTec uses 1,2,3);
+ *   out          (n,) fp32: mean over k of sum_{j in top-k(i)} W_ij s_j / sum W_ij with
+ *                W = X X^T and s the min-max normalised scores.
+ * The reference returns the scores unchanged when k_list contains 0; callers do that
+ * check (the entry point rejects k < 1). */
+int musc_rscin_f32(const float* cls_tokens, const double* image_scores, int n, int d,
+                   const int* k_list, int n_k, float* out, hipStream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* ViT block attention: out = softmax(q k^T * scale) v per (batch*head).      */
 /* ------------------------------------------------------------------------ */

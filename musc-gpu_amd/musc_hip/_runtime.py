@@ -52,6 +52,7 @@ SIGNATURES = {
     'musc_lnamd_f32': (_i, [_vp, _i, _i, _i, _i, _i, _i, _vp, _i, _f, _i, _vp, _i, _vp, _sz, _vp]),
     'musc_maps_f64': (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp]),
     'musc_adaptive_pool_f32': (_i, [_vp, _i, _i, _i, _i, _vp, _vp]),
+    'musc_rscin_f32': (_i, [_vp, _vp, _i, _i, _vp, _i, _vp, _vp]),
     'musc_attention_fwd': (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp]),
     'musc_attention_weights': (_i, [_vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _vp]),
 }

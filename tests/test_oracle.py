@@ -243,3 +243,18 @@ def test_attention_matches_torch_fp32():
     ref = torch.softmax((q / 8.0) @ k.transpose(1, 2), -1) @ v
     got = oa.attention_f64(q.numpy(), k.numpy(), v.numpy(), 1 / 8.0)
     np.testing.assert_allclose(ref.numpy(), got, atol=1e-5)
+
+
+# --------------------------------------------------------------------------- RsCIN
+def test_rscin_oracle_vs_bruteforce_and_closed_forms():
+    from oracle import rscin as orc
+    rng = np.random.default_rng(11)
+    cls = rng.standard_normal((20, 16)).astype(np.float32)
+    cls /= np.linalg.norm(cls, axis=1, keepdims=True)
+    raw = rng.random(20) * 3.0
+    for ks in ([1, 2, 3], [1, 8, 9], [4]):
+        np.testing.assert_allclose(orc.rscin(raw, list(cls), ks), orc.rscin_bruteforce_f64(raw, cls, ks), atol=2e-6)
+    # k = 1 keeps each row's own similarity (1 for unit tokens, the row maximum): scores are just min-max normalised
+    np.testing.assert_allclose(orc.rscin(raw, list(cls), [1]), (raw - raw.min()) / (raw.max() - raw.min()), atol=1e-6)
+    # 0 in k_list or no tokens: unchanged
+    assert orc.rscin(raw, list(cls), [0, 1]) is raw and orc.rscin(raw, None, [1]) is raw
