@@ -4,6 +4,7 @@
     python musc-gpu_amd/musc_hip/kernels_bench.py lnamd [--n 83 --layers 4 --iters 3]
     python musc-gpu_amd/musc_hip/kernels_bench.py attention [--dtype fp32|fp16 --blocks 24]
     python musc-gpu_amd/musc_hip/kernels_bench.py copy [--mib 1024 --iters 3]
+    python musc-gpu_amd/musc_hip/kernels_bench.py e2e --n 160 --iters 1       (config 5)
     python musc-gpu_amd/musc_hip/kernels_bench.py msm lnamd copy --iters 1   (several in one process)
 
 Each prints one JSON line with the average duration of the kernel(s) from HIP
@@ -127,6 +128,30 @@ def bench_attention(args):
             'peak_tflops': peak}
 
 
+def bench_e2e(args):
+    """Config 5: random-init ViT-L/14 at 518 px over N seeded images (5 % with an anomalous
+    rectangle), tokens after blocks 6/12/18/24, LNAMD r 1/3/5, MSM, epilogue, RsCIN."""
+    from musc_hip import pipeline, vit
+    dev = torch.device('cuda:0')
+    torch.manual_seed(0)
+    model = vit.vit_l14(518).to(dev).eval()
+    imgs, anomalous = synthetic.images(n=args.n, size=518, seed=42)
+    imgs = imgs.to(dev)
+    ts = []
+    for it in range(args.iters + 1):
+        timing = {}
+        out = pipeline.run_category(model, imgs, timing=timing)
+        torch.cuda.synchronize()
+        e0, e1, e2, e3 = timing['events'][0]
+        if it > 0:
+            ts.append((e0.elapsed_time(e1), e1.elapsed_time(e2), e2.elapsed_time(e3), e0.elapsed_time(e3)))
+        print(f'[e2e] iteration {it} done', file=sys.stderr, flush=True)
+        del out
+    enc, score, rsc, total = (sum(t[i] for t in ts) / len(ts) for i in range(4))
+    return {'kernel': 'e2e', 'n': args.n, 'encoder_ms': enc, 'lnamd_msm_epilogue_ms': score, 'rscin_ms': rsc,
+            'total_ms': total, 'images_per_s': args.n / (total / 1e3), 'anomalous_images': anomalous}
+
+
 def bench_copy(args):
     dev = torch.device('cuda:0')
     n = args.mib * (1 << 20) // 4
@@ -148,7 +173,7 @@ def bench_copy(args):
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument('kernels', nargs='+', choices=['msm', 'lnamd', 'attention', 'copy'])
+    ap.add_argument('kernels', nargs='+', choices=['msm', 'lnamd', 'attention', 'copy', 'e2e'])
     ap.add_argument('--n', type=int, default=83)
     ap.add_argument('--p', type=int, default=1369)
     ap.add_argument('--c', type=int, default=1024)
@@ -158,7 +183,8 @@ def main():
     ap.add_argument('--mib', type=int, default=1024)
     ap.add_argument('--iters', type=int, default=3)
     args = ap.parse_args()
-    table = {'msm': bench_msm, 'lnamd': bench_lnamd, 'attention': bench_attention, 'copy': bench_copy}
+    table = {'msm': bench_msm, 'lnamd': bench_lnamd, 'attention': bench_attention, 'copy': bench_copy,
+             'e2e': bench_e2e}
     for name in args.kernels:
         print(json.dumps(table[name](args)), flush=True)
 

@@ -26,6 +26,7 @@ from __future__ import annotations
 import torch
 
 from . import _MSM_hip, _epilogue_hip, _lnamd_hip, _super_fast
+from ._RsCIN_hip import RsCIN
 from . import _runtime as rt
 
 
@@ -102,3 +103,47 @@ def score_pool(tokens: list[torch.Tensor], r_list=(1, 3, 5), image_size: int = 5
                      pair_events=timing.setdefault('pairs', []) if timing is not None else None)
     del pools
     return _epilogue_hip.maps_and_scores(scores, image_size, want_maps=want_maps)
+
+
+def run_category(model, images: torch.Tensor, feature_layers=(5, 11, 17, 23), r_list=(1, 3, 5),
+                 batch_size: int = 4, image_size: int | None = None, k_list=(1, 2, 3), autocast: bool = True,
+                 pool_grid: int | None = None, timing: dict | None = None):
+    """One division of MuSc.make_category_data's hot path (models/musc.py:163-296) on the GPU.
+
+    images (N, 3, S, S) normalised GPU tensor -> dict with 'maps' (N, 1, S, S) float64,
+    'image_scores' (N,) float64 map maxima, 'scores' (N,) fp32 after RsCIN, 'class_tokens'
+    (N, D) fp32.  The encoder runs in batches of `batch_size` under fp16 autocast (as at
+    musc.py:196) with the fused attention (musc_hip._encoder_hip); layer tokens stay on
+    the GPU; then LNAMD, MSM, the epilogue and RsCIN run as in score_pool.
+    """
+    from . import _encoder_hip
+
+    n = images.shape[0]
+    image_size = image_size or images.shape[-1]
+    out_layers = [l + 1 for l in feature_layers]               # musc.py:61
+    ev = (lambda: torch.cuda.Event(enable_timing=True)) if timing is not None else None
+    if timing is not None:
+        e0 = ev(); e0.record()
+    _encoder_hip.begin_inference()
+    tokens_per_layer = [[] for _ in out_layers]
+    cls = []
+    with torch.no_grad(), torch.autocast('cuda', dtype=torch.float16, enabled=autocast):
+        for start in range(0, n, batch_size):
+            pooled, toks = _encoder_hip.encode_image(model, images[start:start + batch_size], out_layers)
+            pooled = pooled / pooled.norm(dim=-1, keepdim=True)  # musc.py:215
+            cls.append(pooled.float())
+            for l, t in enumerate(toks):
+                tokens_per_layer[l].append(t)
+    tokens = [torch.cat(t, 0).contiguous() for t in tokens_per_layer]
+    class_tokens = torch.cat(cls, 0)
+    if timing is not None:
+        e1 = ev(); e1.record()
+    maps, image_scores = score_pool(tokens, r_list=r_list, image_size=image_size, pool_grid=pool_grid)
+    if timing is not None:
+        e2 = ev(); e2.record()
+    scores = RsCIN(image_scores, class_tokens, list(k_list))
+    if timing is not None:
+        e3 = ev(); e3.record()
+        timing.setdefault('events', []).append((e0, e1, e2, e3))
+    return {'maps': maps, 'image_scores': image_scores, 'scores': scores, 'class_tokens': class_tokens,
+            'tokens': tokens}

@@ -38,3 +38,26 @@ def pool_tokens(n: int = 83, layers: int = 4, tokens: int = 1370, c: int = 1024,
 def msm_features(n: int, p: int, c: int, seed: int = 42) -> torch.Tensor:
     g = torch.Generator().manual_seed(seed)
     return _normalise(torch.randn((n, p, c), generator=g, dtype=torch.float32))
+
+
+# CLIP image normalisation constants (OpenAI CLIP preprocessing)
+CLIP_MEAN = (0.48145466, 0.4578275, 0.40821073)
+CLIP_STD = (0.26862954, 0.26130258, 0.27577711)
+
+
+def images(n: int = 160, size: int = 518, seed: int = 42, anomaly_fraction: float = 0.05) -> tuple[torch.Tensor, list]:
+    """Config 5: n uniform[0,1] RGB images; round(n * anomaly_fraction) of them carry one
+    random rectangle shifted in intensity.  Returns (CLIP-normalised (n, 3, size, size)
+    fp32, indices of the anomalous images)."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.rand((n, 3, size, size), generator=g)
+    k = int(round(n * anomaly_fraction))
+    idx = torch.randperm(n, generator=g)[:k].tolist()
+    for i in idx:
+        h, w = (int(v) for v in torch.randint(size // 16, size // 4, (2,), generator=g))
+        y0, x0 = (int(v) for v in torch.randint(0, size - max(h, w), (2,), generator=g))
+        shift = float(torch.rand((), generator=g)) * 0.6 + 0.2
+        x[i, :, y0:y0 + h, x0:x0 + w] = (x[i, :, y0:y0 + h, x0:x0 + w] + shift).clamp(0, 1)
+    mean = torch.tensor(CLIP_MEAN).view(1, 3, 1, 1)
+    std = torch.tensor(CLIP_STD).view(1, 3, 1, 1)
+    return (x - mean) / std, sorted(idx)
