@@ -205,6 +205,13 @@ int musc_attention_fwd(const void* q, const void* k, const void* v, void* out,
 int musc_attention_weights(const void* q, const void* k, int dtype, int batch, int heads,
                            int t, int d, float scale, float* weights, hipStream_t stream);
 
+/* Calibration (no counterpart in the reference; a measurement aid): `blocks`
+ * workgroups of 4 waves each issue iters*64 independent v_mfma_f32_32x32x2f32
+ * with no memory traffic, then write one float per thread to out (blocks*256
+ * floats).  *flop (host, may be NULL) receives the FLOP count of the launch, so
+ * flop / time is the sustained fp32 MFMA rate of the device. */
+int musc_calibrate_mfma_f32(float* out, int blocks, int iters, double* flop, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

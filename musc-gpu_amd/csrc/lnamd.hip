@@ -125,6 +125,8 @@ __global__ void lnamd_finalize_kernel(TokenPtrs tokens, int n_layers, int units,
   stats[unit * 2 + 1] = 1.0 / sqrt(var + (double)eps);
 }
 
+typedef float nt_float4 __attribute__((ext_vector_type(4)));
+
 __device__ inline float4 f4add(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
 __device__ inline float4 f4scale(float4 a, float s) { return make_float4(a.x * s, a.y * s, a.z * s, a.w * s); }
 __device__ inline float f4dot(float4 a) { return a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w; }
@@ -376,7 +378,10 @@ __global__ __launch_bounds__(1024) void lnamd_stream_kernel(TokenPtrs tokens, in
           o = ((((long long)ko * batch + b) * P + p) * n_layers + l) * c;
         else
           o = ((((long long)ko * n_layers + l) * batch + b) * P + p) * c;
-        reinterpret_cast<float4*>(out + o)[g] = f4scale(acc, sc);
+        // streaming store: the pools are read back only by later kernels
+        const float4 r = f4scale(acc, sc);
+        const nt_float4 v = {r.x, r.y, r.z, r.w};
+        __builtin_nontemporal_store(v, reinterpret_cast<nt_float4*>(out + o) + g);
       }
     }
   }

@@ -55,6 +55,7 @@ SIGNATURES = {
     'musc_rscin_f32': (_i, [_vp, _vp, _i, _i, _vp, _i, _vp, _vp]),
     'musc_attention_fwd': (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp]),
     'musc_attention_weights': (_i, [_vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _vp]),
+    'musc_calibrate_mfma_f32': (_i, [_vp, _i, _i, ctypes.POINTER(ctypes.c_double), _vp]),
 }
 
 _lock = threading.Lock()

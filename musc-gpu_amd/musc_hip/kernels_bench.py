@@ -5,6 +5,7 @@
     python musc-gpu_amd/musc_hip/kernels_bench.py attention [--dtype fp32|fp16 --blocks 24]
     python musc-gpu_amd/musc_hip/kernels_bench.py copy [--mib 1024 --iters 3]
     python musc-gpu_amd/musc_hip/kernels_bench.py e2e --n 160 --iters 1       (config 5)
+    python musc-gpu_amd/musc_hip/kernels_bench.py mfma_peak                   (device calibration)
     python musc-gpu_amd/musc_hip/kernels_bench.py msm lnamd copy --iters 1   (several in one process)
 
 Each prints one JSON line with the average duration of the kernel(s) from HIP
@@ -152,6 +153,28 @@ def bench_e2e(args):
             'total_ms': total, 'images_per_s': args.n / (total / 1e3), 'anomalous_images': anomalous}
 
 
+def bench_mfma_peak(args):
+    """Sustained fp32 MFMA rate with no memory traffic (musc_calibrate_mfma_f32)."""
+    import ctypes
+    dev = torch.device('cuda:0')
+    blocks = 256 * 8
+    out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    flop = ctypes.c_double()
+    ts = []
+    for it in range(args.iters + 1):
+        e0, e1 = _events()
+        e0.record()
+        rt.check(rt.library().musc_calibrate_mfma_f32(out.data_ptr(), blocks, 2000, ctypes.byref(flop),
+                                                      rt.stream(dev)), 'musc_calibrate_mfma_f32')
+        e1.record()
+        torch.cuda.synchronize()
+        if it > 0:
+            ts.append(e0.elapsed_time(e1))
+    ms = sum(ts) / len(ts)
+    tf = flop.value / (ms / 1e3) / 1e12
+    return {'kernel': 'mfma_peak', 'avg_ms': ms, 'tflops': tf, 'frac_datasheet_peak': tf / FP32_MFMA_TFLOPS}
+
+
 def bench_copy(args):
     dev = torch.device('cuda:0')
     n = args.mib * (1 << 20) // 4
@@ -173,7 +196,7 @@ def bench_copy(args):
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument('kernels', nargs='+', choices=['msm', 'lnamd', 'attention', 'copy', 'e2e'])
+    ap.add_argument('kernels', nargs='+', choices=['msm', 'lnamd', 'attention', 'copy', 'e2e', 'mfma_peak'])
     ap.add_argument('--n', type=int, default=83)
     ap.add_argument('--p', type=int, default=1369)
     ap.add_argument('--c', type=int, default=1024)
@@ -184,7 +207,7 @@ def main():
     ap.add_argument('--iters', type=int, default=3)
     args = ap.parse_args()
     table = {'msm': bench_msm, 'lnamd': bench_lnamd, 'attention': bench_attention, 'copy': bench_copy,
-             'e2e': bench_e2e}
+             'e2e': bench_e2e, 'mfma_peak': bench_mfma_peak}
     for name in args.kernels:
         print(json.dumps(table[name](args)), flush=True)
 
