@@ -52,12 +52,32 @@ __device__ inline void st4(void* base, long long idx4, float4 v) {
   }
 }
 
-template <int kDtype>
-__global__ __launch_bounds__(WAVES * kWave) void attn_fwd_kernel(const void* __restrict__ qg, const void* __restrict__ kg,
-                                                                 const void* __restrict__ vg, void* __restrict__ og,
-                                                                 int t, float scale_log2) {
-  __shared__ __attribute__((aligned(16))) float Ks[KB * KPITCH];
-  __shared__ __attribute__((aligned(16))) float Vt[D * VPITCH];
+// K / V^T staging: each thread loads two float4 of K and two of V per 32-key block
+// (idx = tid + 256*i -> key idx/16, channels 4*(idx%16)) into registers, one block
+// ahead of the compute; the LDS copy is double-buffered so one barrier per block
+// suffices.
+__device__ inline float4 load_kv_row(const float* __restrict__ src, long long head4, int t, int kb, int idx) {
+  const int key = idx / (D / 4), d4 = idx % (D / 4);
+  const int gk = kb * KB + key;
+  return gk < t ? reinterpret_cast<const float4*>(src)[head4 + (long long)gk * (D / 4) + d4]
+                : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+__device__ inline void store_kv_row(float* __restrict__ Ks, float* __restrict__ Vt, int idx, float4 kv, float4 vv) {
+  const int key = idx / (D / 4), d4 = (idx % (D / 4)) * 4;
+  *reinterpret_cast<float4*>(&Ks[key * KPITCH + d4]) = kv;
+  Vt[(d4 + 0) * VPITCH + key] = vv.x;
+  Vt[(d4 + 1) * VPITCH + key] = vv.y;
+  Vt[(d4 + 2) * VPITCH + key] = vv.z;
+  Vt[(d4 + 3) * VPITCH + key] = vv.w;
+}
+
+__global__ __launch_bounds__(WAVES * kWave, 3) void attn_fwd_kernel(const float* __restrict__ qg,
+                                                                 const float* __restrict__ kg,
+                                                                 const float* __restrict__ vg,
+                                                                 float* __restrict__ og, int t, float scale_log2) {
+  __shared__ __attribute__((aligned(16))) float Ks[2][KB * KPITCH];
+  __shared__ __attribute__((aligned(16))) float Vt[2][D * VPITCH];
 
   const int bh = blockIdx.y;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
@@ -71,7 +91,8 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_kernel(const void* __r
     const bool ok = q < t;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      float4 v = ok ? ld4<kDtype>(qg, head4 + (long long)q * (D / 4) + 2 * s + lh) : make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 v = ok ? reinterpret_cast<const float4*>(qg)[head4 + (long long)q * (D / 4) + 2 * s + lh]
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
       qr[s][0] = v.x * scale_log2;
       qr[s][1] = v.y * scale_log2;
       qr[s][2] = v.z * scale_log2;
@@ -88,23 +109,21 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_kernel(const void* __r
   float m = -INFINITY, l = 0.f;
 
   const int nkb = (t + KB - 1) / KB;
+  // K / V^T staging: thread tid moves elements idx = tid and tid + 256 of each
+  // 32-key block (key idx/16, channels 4*(idx%16)), loaded one block ahead; the LDS
+  // copy is double-buffered, so one barrier per block suffices.
+  const int i0 = threadIdx.x, i1 = threadIdx.x + WAVES * kWave;
+  float4 k0 = load_kv_row(kg, head4, t, 0, i0), k1 = load_kv_row(kg, head4, t, 0, i1);
+  float4 v0 = load_kv_row(vg, head4, t, 0, i0), v1 = load_kv_row(vg, head4, t, 0, i1);
   for (int kb = 0; kb < nkb; ++kb) {
-    // stage K (row-major) and V^T for keys kb*KB .. +KB
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int idx = threadIdx.x + i * WAVES * kWave;  // 0..511
-      const int key = idx / (D / 4), d4 = (idx % (D / 4)) * 4;
-      const int gk = kb * KB + key;
-      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-      if (gk < t) {
-        kv = ld4<kDtype>(kg, head4 + (long long)gk * (D / 4) + d4 / 4);
-        vv = ld4<kDtype>(vg, head4 + (long long)gk * (D / 4) + d4 / 4);
-      }
-      *reinterpret_cast<float4*>(&Ks[key * KPITCH + d4]) = kv;
-      Vt[(d4 + 0) * VPITCH + key] = vv.x;
-      Vt[(d4 + 1) * VPITCH + key] = vv.y;
-      Vt[(d4 + 2) * VPITCH + key] = vv.z;
-      Vt[(d4 + 3) * VPITCH + key] = vv.w;
+    const int buf = kb & 1;
+    store_kv_row(Ks[buf], Vt[buf], i0, k0, v0);
+    store_kv_row(Ks[buf], Vt[buf], i1, k1, v1);
+    if (kb + 1 < nkb) {
+      k0 = load_kv_row(kg, head4, t, kb + 1, i0);
+      k1 = load_kv_row(kg, head4, t, kb + 1, i1);
+      v0 = load_kv_row(vg, head4, t, kb + 1, i0);
+      v1 = load_kv_row(vg, head4, t, kb + 1, i1);
     }
     __syncthreads();
 
@@ -112,7 +131,7 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_kernel(const void* __r
     floatx16 s;
 #pragma unroll
     for (int v = 0; v < 16; ++v) s[v] = 0.f;
-    const float* krow = &Ks[lq * KPITCH + 4 * lh];
+    const float* krow = &Ks[buf][lq * KPITCH + 4 * lh];
 #pragma unroll
     for (int ss = 0; ss < 8; ++ss) {
       const float4 a = *reinterpret_cast<const float4*>(krow + 8 * ss);
@@ -121,17 +140,17 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_kernel(const void* __r
       s = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, qr[ss][2], s, 0, 0, 0);
       s = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, qr[ss][3], s, 0, 0, 0);
     }
-    // mask keys beyond t; register v holds key (v/4)*8 + 4h + v%4 of the block
-    float bmax = -INFINITY;
+    // register v holds key (v/4)*8 + 4h + v%4 of the block; only the last block is ragged
+    if ((kb + 1) * KB > t) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int key = kb * KB + (v >> 2) * 8 + lh * 4 + (v & 3);
-      if (key >= t) s[v] = -INFINITY;
-      bmax = fmaxf(bmax, s[v]);
+      for (int v = 0; v < 16; ++v)
+        if (kb * KB + (v >> 2) * 8 + lh * 4 + (v & 3) >= t) s[v] = -INFINITY;
     }
+    float bmax = s[0];
+#pragma unroll
+    for (int v = 1; v < 16; ++v) bmax = fmaxf(bmax, s[v]);
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
     const float mnew = fmaxf(m, bmax);
-    const float alpha = exp2f(m - mnew);  // 0 on the first block (m = -inf)
     float psum = 0.f;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
@@ -139,16 +158,20 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_kernel(const void* __r
       psum += s[v];
     }
     psum += __shfl_xor(psum, 32, kWave);
-    l = l * alpha + psum;
-    m = mnew;
+    if (!__all(mnew == m)) {  // rescale only when some running maximum moved
+      const float alpha = exp2f(m - mnew);  // 0 on the first block (m = -inf)
+      l *= alpha;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      o0[v] *= alpha;
-      o1[v] *= alpha;
+      for (int v = 0; v < 16; ++v) {
+        o0[v] *= alpha;
+        o1[v] *= alpha;
+      }
     }
+    l += psum;
+    m = mnew;
     // O^T += V^T P^T ; step e uses key 8*(e/4) + 4h + e%4 = register e of s
-    const float* vrow0 = &Vt[lq * VPITCH + 4 * lh];
-    const float* vrow1 = &Vt[(32 + lq) * VPITCH + 4 * lh];
+    const float* vrow0 = &Vt[buf][lq * VPITCH + 4 * lh];
+    const float* vrow1 = &Vt[buf][(32 + lq) * VPITCH + 4 * lh];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float4 a0 = *reinterpret_cast<const float4*>(vrow0 + 8 * j);
@@ -162,7 +185,6 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_kernel(const void* __r
       o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.w, s[4 * j + 3], o0, 0, 0, 0);
       o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.w, s[4 * j + 3], o1, 0, 0, 0);
     }
-    __syncthreads();
   }
 
   if (q < t) {
@@ -172,8 +194,8 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_kernel(const void* __r
     for (int g = 0; g < 4; ++g) {
       const float4 a = make_float4(o0[4 * g] * inv, o0[4 * g + 1] * inv, o0[4 * g + 2] * inv, o0[4 * g + 3] * inv);
       const float4 b = make_float4(o1[4 * g] * inv, o1[4 * g + 1] * inv, o1[4 * g + 2] * inv, o1[4 * g + 3] * inv);
-      st4<kDtype>(og, head4 + (long long)q * (D / 4) + (8 * g + 4 * lh) / 4, a);
-      st4<kDtype>(og, head4 + (long long)q * (D / 4) + (32 + 8 * g + 4 * lh) / 4, b);
+      reinterpret_cast<float4*>(og)[head4 + (long long)q * (D / 4) + (8 * g + 4 * lh) / 4] = a;
+      reinterpret_cast<float4*>(og)[head4 + (long long)q * (D / 4) + (32 + 8 * g + 4 * lh) / 4] = b;
     }
   }
 }
@@ -195,8 +217,8 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
                                                                      const _Float16* __restrict__ vg,
                                                                      _Float16* __restrict__ og, int t,
                                                                      float scale_log2) {
-  __shared__ __attribute__((aligned(16))) _Float16 Ks[KB * KP16];
-  __shared__ __attribute__((aligned(16))) _Float16 Vt[D * VP16];
+  __shared__ __attribute__((aligned(16))) _Float16 Ks[2][KB * KP16];
+  __shared__ __attribute__((aligned(16))) _Float16 Vt[2][D * VP16];
 
   const int bh = blockIdx.y;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
@@ -227,26 +249,37 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
 
   const int nkb = (t + KB - 1) / KB;
   const int tid = threadIdx.x;
+  // staging: thread tid moves K row tid/8, halves 8*(tid%8).. (16 B) and V rows
+  // 2*(tid/16), 2*(tid/16)+1, halves 4*(tid%16).. (8 B each), one block ahead
+  const int skey = tid / 8, sd8 = (tid % 8) * 8;
+  const int kp = tid / 16, dg = tid % 16;
+  auto load_k = [&](int kb) -> half8 {
+    const int gk = kb * KB + skey;
+    half8 r = {};
+    if (gk < t) r = *reinterpret_cast<const half8*>(kg + head + (long long)gk * D + sd8);
+    return r;
+  };
+  auto load_v = [&](int kb, int which) -> half4 {
+    const int gk = kb * KB + 2 * kp + which;
+    half4 r = {};
+    if (gk < t) r = *reinterpret_cast<const half4*>(vg + head + (long long)gk * D + 4 * dg);
+    return r;
+  };
+  half8 kreg = load_k(0);
+  half4 v0 = load_v(0, 0), v1 = load_v(0, 1);
   for (int kb = 0; kb < nkb; ++kb) {
-    {
-      // K: 32 keys x 64 d, 8 halves per thread
-      const int key = tid / 8, d8 = (tid % 8) * 8;
-      const int gk = kb * KB + key;
-      half8 kv = {};
-      if (gk < t) kv = *reinterpret_cast<const half8*>(kg + head + (long long)gk * D + d8);
-      *reinterpret_cast<half8*>(&Ks[key * KP16 + d8]) = kv;
-      // V^T: keys 2kp, 2kp+1 x d 4dg..4dg+3 per thread, written as key pairs
-      const int kp = tid / 16, dg = tid % 16;
-      const int gk0 = kb * KB + 2 * kp, gk1 = gk0 + 1;
-      half4 v0 = {}, v1 = {};
-      if (gk0 < t) v0 = *reinterpret_cast<const half4*>(vg + head + (long long)gk0 * D + 4 * dg);
-      if (gk1 < t) v1 = *reinterpret_cast<const half4*>(vg + head + (long long)gk1 * D + 4 * dg);
+    const int buf = kb & 1;
+    *reinterpret_cast<half8*>(&Ks[buf][skey * KP16 + sd8]) = kreg;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-        half2v pr = {v0[i], v1[i]};
-        *reinterpret_cast<half2v*>(&Vt[(4 * dg + i) * VP16 + 2 * kp]) = pr;
-      }
+    for (int i = 0; i < 4; ++i) {
+      typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+      half2v pr = {v0[i], v1[i]};
+      *reinterpret_cast<half2v*>(&Vt[buf][(4 * dg + i) * VP16 + 2 * kp]) = pr;
+    }
+    if (kb + 1 < nkb) {
+      kreg = load_k(kb + 1);
+      v0 = load_v(kb + 1, 0);
+      v1 = load_v(kb + 1, 1);
     }
     __syncthreads();
 
@@ -255,19 +288,19 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
     for (int v = 0; v < 16; ++v) s[v] = 0.f;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      const half8 a = *reinterpret_cast<const half8*>(&Ks[lq * KP16 + 16 * m + 8 * lh]);
+      const half8 a = *reinterpret_cast<const half8*>(&Ks[buf][lq * KP16 + 16 * m + 8 * lh]);
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[m], s, 0, 0, 0);
     }
-    float bmax = -INFINITY;
+    if ((kb + 1) * KB > t) {  // only the last block is ragged
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int key = kb * KB + (v >> 2) * 8 + lh * 4 + (v & 3);
-      if (key >= t) s[v] = -INFINITY;
-      bmax = fmaxf(bmax, s[v]);
+      for (int v = 0; v < 16; ++v)
+        if (kb * KB + (v >> 2) * 8 + lh * 4 + (v & 3) >= t) s[v] = -INFINITY;
     }
+    float bmax = s[0];
+#pragma unroll
+    for (int v = 1; v < 16; ++v) bmax = fmaxf(bmax, s[v]);
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
     const float mnew = fmaxf(m_run, bmax);
-    const float alpha = exp2f(m_run - mnew);
     float psum = 0.f;
     half8 pf[2];
 #pragma unroll
@@ -277,25 +310,28 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
       pf[v >> 3][v & 7] = (_Float16)e;
     }
     psum += __shfl_xor(psum, 32, kWave);
-    l_run = l_run * alpha + psum;
+    if (!__all(mnew == m_run)) {  // rescale only when some running maximum moved
+      const float alpha = exp2f(m_run - mnew);
+      l_run *= alpha;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        o0[v] *= alpha;
+        o1[v] *= alpha;
+      }
+    }
+    l_run += psum;
     m_run = mnew;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      o0[v] *= alpha;
-      o1[v] *= alpha;
-    }
-#pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
-      const half4 a0l = *reinterpret_cast<const half4*>(&Vt[lq * VP16 + 16 * mm + 4 * lh]);
-      const half4 a0h = *reinterpret_cast<const half4*>(&Vt[lq * VP16 + 16 * mm + 8 + 4 * lh]);
-      const half4 a1l = *reinterpret_cast<const half4*>(&Vt[(32 + lq) * VP16 + 16 * mm + 4 * lh]);
-      const half4 a1h = *reinterpret_cast<const half4*>(&Vt[(32 + lq) * VP16 + 16 * mm + 8 + 4 * lh]);
+      const half4 a0l = *reinterpret_cast<const half4*>(&Vt[buf][lq * VP16 + 16 * mm + 4 * lh]);
+      const half4 a0h = *reinterpret_cast<const half4*>(&Vt[buf][lq * VP16 + 16 * mm + 8 + 4 * lh]);
+      const half4 a1l = *reinterpret_cast<const half4*>(&Vt[buf][(32 + lq) * VP16 + 16 * mm + 4 * lh]);
+      const half4 a1h = *reinterpret_cast<const half4*>(&Vt[buf][(32 + lq) * VP16 + 16 * mm + 8 + 4 * lh]);
       const half8 a0 = {a0l[0], a0l[1], a0l[2], a0l[3], a0h[0], a0h[1], a0h[2], a0h[3]};
       const half8 a1 = {a1l[0], a1l[1], a1l[2], a1l[3], a1h[0], a1h[1], a1h[2], a1h[3]};
       o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, pf[mm], o0, 0, 0, 0);
       o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, pf[mm], o1, 0, 0, 0);
     }
-    __syncthreads();
   }
 
   if (q < t) {
@@ -402,8 +438,9 @@ extern "C" int musc_attention_fwd(const void* q, const void* k, const void* v, v
   const float scale_log2 = scale * 1.4426950408889634f;
   dim3 grid((t + attn::QW * attn::WAVES - 1) / (attn::QW * attn::WAVES), bh);
   if (dtype == MUSC_DTYPE_F32)
-    hipLaunchKernelGGL(attn::attn_fwd_kernel<MUSC_DTYPE_F32>, grid, dim3(attn::WAVES * kWave), 0, stream, q, k, v, out,
-                       t, scale_log2);
+    hipLaunchKernelGGL(attn::attn_fwd_kernel, grid, dim3(attn::WAVES * kWave), 0, stream,
+                       static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
+                       static_cast<float*>(out), t, scale_log2);
   else
     hipLaunchKernelGGL(attn::attn_fwd_f16_kernel, grid, dim3(attn::WAVES * kWave), 0, stream,
                        static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
