@@ -163,13 +163,31 @@ def main() -> int:
         log(f'[bench] warmup step {w + 1}/{args.warmup} done')
 
     timing: dict = {}
+    step_ev = []
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s in range(args.steps):
+        ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        ev[0].record()
         maps, img = pipeline.score_pool(tokens, r_list, image_size, timing=timing)
+        ev[1].record()
+        step_ev.append(ev)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     log(f'[bench] {args.steps} timed steps in {elapsed:.3f} s')
+    step_ms = sorted(a.elapsed_time(b) for a, b in step_ev)
+    median_ms = step_ms[len(step_ms) // 2]
+
+    # One extra step with the tokens starting in pinned host memory (outside the
+    # timed region; reported separately, never as `value`).
+    pinned = [t.pin_memory() for t in tokens_cpu]
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    dev_tokens = [t.to(dev, non_blocking=True) for t in pinned]
+    pipeline.score_pool(dev_tokens, r_list, image_size)
+    torch.cuda.synchronize()
+    h2d_step_s = time.perf_counter() - t1
+    del dev_tokens, pinned
 
     pair_ms = [a.elapsed_time(b) for a, b in timing['pairs']]
     lnamd_ms = [a.elapsed_time(b) for a, b in timing['lnamd']]
@@ -188,6 +206,8 @@ def main() -> int:
         'steps': args.steps,
         'warmup': args.warmup,
         'ms_per_step': elapsed / args.steps * 1e3,
+        'median_ms_per_step': median_ms,
+        'h2d_inclusive_images_per_s': n / h2d_step_s,
         'higher_is_better': True,
         'scaling': 'weak',
         'vs_baseline': None,
