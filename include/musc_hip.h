@@ -199,11 +199,17 @@ int musc_attention_fwd(const void* q, const void* k, const void* v, void* out,
 
 /* Head-averaged attention probabilities:
  *   weights (batch, t, t) fp32 out, weights[b][i][j] = mean over heads h of
- *   softmax_j(q[b*heads+h][i] . k[b*heads+h][j] * scale); q, k (batch*heads, t, d).
+ *   softmax_j(q[b*heads+h][i] . k[b*heads+h][j] * scale); q, k (batch*heads, t, d),
+ *   fp32 or fp16 (dtype), logits and probabilities in fp32.
  * Serves the one block whose weights the encoder reads (need_weights=True,
- * models/backbone/open_clip/transformer.py:232-234,331-333).  d = 64, t <= 2048. */
+ * models/backbone/open_clip/transformer.py:232-234,331-333; the fp32 softmax the
+ * reference keeps for that block, models/modules/_attention_gpu.py:41-81).
+ * Workspace: musc_attention_weights_workspace_bytes (per-(head, query) softmax
+ * statistics), 8-byte aligned.  d = 64, batch*heads <= 65535. */
+int musc_attention_weights_workspace_bytes(int batch, int heads, int t, size_t* out);
 int musc_attention_weights(const void* q, const void* k, int dtype, int batch, int heads,
-                           int t, int d, float scale, float* weights, hipStream_t stream);
+                           int t, int d, float scale, float* weights,
+                           void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Calibration (no counterpart in the reference; a measurement aid): `blocks`
  * workgroups of 4 waves each issue iters*64 independent v_mfma_f32_32x32x2f32

@@ -348,75 +348,170 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
 
 // Head-averaged attention probabilities, for the one block whose weights the
 // caller reads (models/backbone/open_clip/transformer.py:331-333, averaged by
-// nn.MultiheadAttention over heads).  One workgroup per (batch, query row); each
-// thread owns keys tid, tid + 256, ... and accumulates mean_h softmax_h there.
-constexpr int kWMaxKeysPerThread = 8;   // t <= 2048
-
+// nn.MultiheadAttention over heads): weights[b, i, j] = mean_h softmax_j(scale *
+// q[b,h,i] . k[b,h,j]), fp32 logits and probabilities.
+//
+// Two passes on MFMA, both in the S^T = K Q^T layout (lane owns one query):
+//   attn_wstats_kernel    one wave per (batch*head, 32 queries): running max and
+//                         sum over all key blocks -> (max, 1/sum) per query, in
+//                         the exp2 domain with the scale folded in.
+//   attn_weights_kernel   one wave per (batch, 32 queries, kKR key blocks): for
+//                         every head recomputes the logits of its key blocks,
+//                         adds exp2(s - max) / sum into registers, then writes
+//                         the averaged rows through an LDS transpose (each store
+//                         instruction covers two 128-byte query-row segments).
+// fp16 inputs use v_mfma_f32_32x32x16_f16 (products exact, fp32 accumulation);
+// fp32 inputs use v_mfma_f32_32x32x2f32 with the same reduction-index split as
+// attn_fwd_kernel.
 template <int kDtype>
-__global__ __launch_bounds__(256) void attn_weights_kernel(const void* __restrict__ qg, const void* __restrict__ kg,
-                                                           int heads, int t, float scale,
-                                                           float* __restrict__ weights) {
-  const int b = blockIdx.x / t, i = blockIdx.x % t;
-  const int tid = threadIdx.x;
-  __shared__ float qrow[D];
-  __shared__ float red[256 / kWave];
-  float acc[kWMaxKeysPerThread];
+struct QFrag;
+template <>
+struct QFrag<MUSC_DTYPE_F16> {
+  half8 v[4];
+};
+template <>
+struct QFrag<MUSC_DTYPE_F32> {
+  float4 v[8];
+};
+
+// Fragment of row `row` (zeros when row >= t) of a (t, 64) head matrix for lane
+// half lh: fp16 -> halves 16m + 8lh .. +7 for m = 0..3; fp32 -> floats 8s + 4lh ..
+// +3 for s = 0..7.
+template <int kDtype>
+__device__ inline QFrag<kDtype> load_frag(const void* base, long long head, int row, int t, int lh) {
+  QFrag<kDtype> f;
+  const bool ok = row < t;
+  if constexpr (kDtype == MUSC_DTYPE_F16) {
+    const _Float16* p = static_cast<const _Float16*>(base) + head + (long long)row * D + 8 * lh;
 #pragma unroll
-  for (int m = 0; m < kWMaxKeysPerThread; ++m) acc[m] = 0.f;
-  for (int h = 0; h < heads; ++h) {
-    const long long head4 = ((long long)(b * heads + h) * t) * (D / 4);
-    __syncthreads();
-    if (tid < D / 4) {
-      const float4 v = ld4<kDtype>(qg, head4 + (long long)i * (D / 4) + tid);
-      qrow[4 * tid + 0] = v.x * scale;
-      qrow[4 * tid + 1] = v.y * scale;
-      qrow[4 * tid + 2] = v.z * scale;
-      qrow[4 * tid + 3] = v.w * scale;
+    for (int m = 0; m < 4; ++m) {
+      half8 v = {};
+      if (ok) v = *reinterpret_cast<const half8*>(p + 16 * m);
+      f.v[m] = v;
     }
-    __syncthreads();
-    float lg[kWMaxKeysPerThread];
-    float mx = -INFINITY;
+  } else {
+    const float* p = static_cast<const float*>(base) + head + (long long)row * D + 4 * lh;
 #pragma unroll
-    for (int m = 0; m < kWMaxKeysPerThread; ++m) {
-      const int j = tid + 256 * m;
-      float dot = -INFINITY;
-      if (j < t) {
-        dot = 0.f;
-#pragma unroll
-        for (int d4 = 0; d4 < D / 4; ++d4) {
-          const float4 kv = ld4<kDtype>(kg, head4 + (long long)j * (D / 4) + d4);
-          dot = fmaf(qrow[4 * d4 + 0], kv.x, dot);
-          dot = fmaf(qrow[4 * d4 + 1], kv.y, dot);
-          dot = fmaf(qrow[4 * d4 + 2], kv.z, dot);
-          dot = fmaf(qrow[4 * d4 + 3], kv.w, dot);
-        }
-      }
-      lg[m] = dot;
-      mx = fmaxf(mx, dot);
-    }
-    mx = wave_max(mx);
-    if (tid % kWave == 0) red[tid / kWave] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float sum = 0.f;
-#pragma unroll
-    for (int m = 0; m < kWMaxKeysPerThread; ++m) {
-      lg[m] = (tid + 256 * m < t) ? expf(lg[m] - mx) : 0.f;
-      sum += lg[m];
-    }
-    sum = wave_sum(sum);
-    __syncthreads();
-    if (tid % kWave == 0) red[tid / kWave] = sum;
-    __syncthreads();
-    sum = red[0] + red[1] + red[2] + red[3];
-#pragma unroll
-    for (int m = 0; m < kWMaxKeysPerThread; ++m) acc[m] += lg[m] / sum;
+    for (int s = 0; s < 8; ++s) f.v[s] = ok ? *reinterpret_cast<const float4*>(p + 8 * s) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  float* dst = weights + ((long long)b * t + i) * t;
+  return f;
+}
+
+// S^T tile (32 keys x 32 queries) of one key block: lane (lq, lh) gets query lq and
+// keys (v/4)*8 + 4lh + v%4 of the block.
+template <int kDtype>
+__device__ inline floatx16 logits_t(const QFrag<kDtype>& kf, const QFrag<kDtype>& qf) {
+  floatx16 s;
 #pragma unroll
-  for (int m = 0; m < kWMaxKeysPerThread; ++m) {
-    const int j = tid + 256 * m;
-    if (j < t) dst[j] = acc[m] / (float)heads;
+  for (int v = 0; v < 16; ++v) s[v] = 0.f;
+  if constexpr (kDtype == MUSC_DTYPE_F16) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf.v[m], qf.v[m], s, 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.v[j].x, qf.v[j].x, s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.v[j].y, qf.v[j].y, s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.v[j].z, qf.v[j].z, s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.v[j].w, qf.v[j].w, s, 0, 0, 0);
+    }
+  }
+  return s;
+}
+
+// grid (ceil(t/32), batch*heads), one wave.  stats[bh*t + i] = (max, 1/sum).
+template <int kDtype>
+__global__ __launch_bounds__(kWave) void attn_wstats_kernel(const void* __restrict__ qg, const void* __restrict__ kg,
+                                                            int t, float scale_log2, float2* __restrict__ stats) {
+  const int bh = blockIdx.y;
+  const int lane = threadIdx.x, lq = lane & 31, lh = lane >> 5;
+  const int query = blockIdx.x * 32 + lq;
+  const long long head = (long long)bh * t * D;
+  const QFrag<kDtype> qf = load_frag<kDtype>(qg, head, query, t, lh);
+  const int nkb = (t + KB - 1) / KB;
+  float m_run = -INFINITY, l_run = 0.f;
+  QFrag<kDtype> kf = load_frag<kDtype>(kg, head, lq, t, lh);
+  for (int kb = 0; kb < nkb; ++kb) {
+    floatx16 s = logits_t<kDtype>(kf, qf);
+    if (kb + 1 < nkb) kf = load_frag<kDtype>(kg, head, (kb + 1) * KB + lq, t, lh);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) s[v] *= scale_log2;
+    if ((kb + 1) * KB > t) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        if (kb * KB + (v >> 2) * 8 + lh * 4 + (v & 3) >= t) s[v] = -INFINITY;
+    }
+    float bmax = s[0];
+#pragma unroll
+    for (int v = 1; v < 16; ++v) bmax = fmaxf(bmax, s[v]);
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+    const float mnew = fmaxf(m_run, bmax);
+    float psum = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) psum += exp2f(s[v] - mnew);
+    psum += __shfl_xor(psum, 32, kWave);
+    l_run = l_run * exp2f(m_run - mnew) + psum;
+    m_run = mnew;
+  }
+  if (lh == 0 && query < t) stats[(long long)bh * t + query] = make_float2(m_run, 1.f / l_run);
+}
+
+// grid (ceil(t/32), ceil(nkb/kKR), batch), one wave.
+template <int kDtype, int kKR>
+__global__ __launch_bounds__(kWave) void attn_weights_kernel(const void* __restrict__ qg, const void* __restrict__ kg,
+                                                             int heads, int t, float scale_log2,
+                                                             const float2* __restrict__ stats,
+                                                             float* __restrict__ weights) {
+  __shared__ float tile[32][33];
+  const int b = blockIdx.z;
+  const int lane = threadIdx.x, lq = lane & 31, lh = lane >> 5;
+  const int q0 = blockIdx.x * 32, query = q0 + lq;
+  const int nkb = (t + KB - 1) / KB;
+  const int kb0 = blockIdx.y * kKR;
+  const int nr = min(kKR, nkb - kb0);
+  floatx16 acc[kKR];
+#pragma unroll
+  for (int r = 0; r < kKR; ++r)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[r][v] = 0.f;
+  for (int h = 0; h < heads; ++h) {
+    const long long head = ((long long)b * heads + h) * t * D;
+    const QFrag<kDtype> qf = load_frag<kDtype>(qg, head, query, t, lh);
+    float mx = 0.f, il = 0.f;  // rows past t contribute nothing and are not written
+    if (query < t) {
+      const float2 st = stats[((long long)b * heads + h) * t + query];
+      mx = st.x;
+      il = st.y;
+    }
+#pragma unroll
+    for (int r = 0; r < kKR; ++r) {
+      if (r < nr) {
+        const int kb = kb0 + r;
+        const QFrag<kDtype> kf = load_frag<kDtype>(kg, head, kb * KB + lq, t, lh);
+        const floatx16 s = logits_t<kDtype>(kf, qf);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[r][v] += exp2f(s[v] * scale_log2 - mx) * il;
+      }
+    }
+  }
+  const float inv_h = 1.f / (float)heads;
+#pragma unroll
+  for (int r = 0; r < kKR; ++r) {
+    if (r < nr) {
+      const int kb = kb0 + r;
+      // tile[query][key] from the S^T registers, then 32 consecutive keys of two
+      // query rows per store instruction
+#pragma unroll
+      for (int v = 0; v < 16; ++v) tile[lq][(v >> 2) * 8 + lh * 4 + (v & 3)] = acc[r][v] * inv_h;
+      __syncthreads();
+      const int key = kb * KB + lq;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = 2 * i + lh;
+        if (q0 + row < t && key < t) weights[((long long)b * t + q0 + row) * t + key] = tile[row][lq];
+      }
+      __syncthreads();
+    }
   }
 }
 
@@ -448,19 +543,39 @@ extern "C" int musc_attention_fwd(const void* q, const void* k, const void* v, v
   return check_launch();
 }
 
+extern "C" int musc_attention_weights_workspace_bytes(int batch, int heads, int t, size_t* out) {
+  if (!out || batch < 1 || heads < 1 || t < 1) return MUSC_ERR_INVALID_ARG;
+  *out = align_up((size_t)batch * heads * t * sizeof(float2), 256);
+  return MUSC_OK;
+}
+
 extern "C" int musc_attention_weights(const void* q, const void* k, int dtype, int batch, int heads, int t, int d,
-                                      float scale, float* weights, hipStream_t stream) {
+                                      float scale, float* weights, void* workspace, size_t workspace_bytes,
+                                      hipStream_t stream) {
   if (!q || !k || !weights || batch < 1 || heads < 1 || t < 1) return MUSC_ERR_INVALID_ARG;
   if (dtype != MUSC_DTYPE_F32 && dtype != MUSC_DTYPE_F16) return MUSC_ERR_INVALID_ARG;
-  if (d != attn::D || t > 256 * attn::kWMaxKeysPerThread) return MUSC_ERR_UNSUPPORTED;
+  if (d != attn::D) return MUSC_ERR_UNSUPPORTED;
   if (((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k)) % 16) != 0) return MUSC_ERR_INVALID_ARG;
-  const long long rows = (long long)batch * t;
-  if (rows > 0x7fffffffLL) return MUSC_ERR_UNSUPPORTED;
-  if (dtype == MUSC_DTYPE_F32)
-    hipLaunchKernelGGL(attn::attn_weights_kernel<MUSC_DTYPE_F32>, dim3((unsigned)rows), dim3(256), 0, stream, q, k,
-                       heads, t, scale, weights);
-  else
-    hipLaunchKernelGGL(attn::attn_weights_kernel<MUSC_DTYPE_F16>, dim3((unsigned)rows), dim3(256), 0, stream, q, k,
-                       heads, t, scale, weights);
+  if (batch > 65535 || (long long)batch * heads > 65535) return MUSC_ERR_UNSUPPORTED;
+  const size_t need = align_up((size_t)batch * heads * t * sizeof(float2), 256);
+  if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) % 8) != 0)
+    return MUSC_ERR_WORKSPACE;
+  float2* stats = static_cast<float2*>(workspace);
+  const float scale_log2 = scale * 1.4426950408889634f;
+  const int nqb = (t + 31) / 32, nkb = (t + attn::KB - 1) / attn::KB;
+  const dim3 sgrid(nqb, batch * heads);
+  if (dtype == MUSC_DTYPE_F32) {
+    constexpr int kKR = 4;
+    hipLaunchKernelGGL(attn::attn_wstats_kernel<MUSC_DTYPE_F32>, sgrid, dim3(kWave), 0, stream, q, k, t, scale_log2,
+                       stats);
+    hipLaunchKernelGGL((attn::attn_weights_kernel<MUSC_DTYPE_F32, kKR>), dim3(nqb, (nkb + kKR - 1) / kKR, batch),
+                       dim3(kWave), 0, stream, q, k, heads, t, scale_log2, stats, weights);
+  } else {
+    constexpr int kKR = 8;
+    hipLaunchKernelGGL(attn::attn_wstats_kernel<MUSC_DTYPE_F16>, sgrid, dim3(kWave), 0, stream, q, k, t, scale_log2,
+                       stats);
+    hipLaunchKernelGGL((attn::attn_weights_kernel<MUSC_DTYPE_F16, kKR>), dim3(nqb, (nkb + kKR - 1) / kKR, batch),
+                       dim3(kWave), 0, stream, q, k, heads, t, scale_log2, stats, weights);
+  }
   return check_launch();
 }

@@ -7,6 +7,8 @@ models/modules/_attention_gpu.py:41-81) never reach HBM.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _runtime as rt
@@ -37,14 +39,19 @@ def attention_weights(q: torch.Tensor, k: torch.Tensor, heads: int, scale: float
     if q.shape != k.shape or q.ndim != 3 or q.dtype != k.dtype or q.dtype not in (torch.float32, torch.float16):
         raise ValueError('q and k must share one (B*H, T, D) float32/float16 shape')
     bh, t, d = q.shape
-    if bh % heads:
+    if heads < 1 or bh % heads:
         raise ValueError('leading dimension must be batch * heads')
     q, k = q.contiguous(), k.contiguous()
+    lib = rt.library()
+    need = ctypes.c_size_t()
+    rt.check(lib.musc_attention_weights_workspace_bytes(bh // heads, heads, t, ctypes.byref(need)),
+             'musc_attention_weights_workspace_bytes')
     with torch.cuda.device(q.device):
         out = torch.empty((bh // heads, t, t), dtype=torch.float32, device=q.device)
-        rc = rt.library().musc_attention_weights(q.data_ptr(), k.data_ptr(),
-                                                 rt.DTYPE_F32 if q.dtype == torch.float32 else rt.DTYPE_F16,
-                                                 bh // heads, heads, t, d, float(scale), out.data_ptr(),
-                                                 rt.stream(q.device))
+        ws = torch.empty(need.value, dtype=torch.uint8, device=q.device)
+        rc = lib.musc_attention_weights(q.data_ptr(), k.data_ptr(),
+                                        rt.DTYPE_F32 if q.dtype == torch.float32 else rt.DTYPE_F16,
+                                        bh // heads, heads, t, d, float(scale), out.data_ptr(),
+                                        ws.data_ptr(), need.value, rt.stream(q.device))
         rt.check(rc, 'musc_attention_weights')
     return out

@@ -54,10 +54,16 @@ def test_vit_l14_full_size_block_tokens(device):
     torch.testing.assert_close(got[0], ref[0], rtol=1e-3, atol=1e-3)
 
 
-def test_attention_weights_kernel(device):
-    g = torch.Generator().manual_seed(5)
-    b, h, t = 2, 16, 300
-    q, k = (torch.randn((b * h, t, 64), generator=g) * 0.5 for _ in range(2))
+@pytest.mark.parametrize('t', [1, 31, 300, 1370])
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float16])
+def test_attention_weights_kernel(device, t, dtype):
+    # vs the float64 head-averaged softmax of the same (rounded) inputs; rows sum to 1
+    g = torch.Generator().manual_seed(5 + t)
+    b, h = 2, 16
+    q, k = ((torch.randn((b * h, t, 64), generator=g) * 0.5).to(dtype) for _ in range(2))
     got = _attention_hip.attention_weights(q.to(device), k.to(device), h, 0.125).cpu()
-    ref = torch.softmax((q * 0.125) @ k.transpose(1, 2), -1).reshape(b, h, t, t).mean(1)
-    torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-6)
+    q64, k64 = q.double(), k.double()
+    ref = torch.softmax((q64 @ k64.transpose(1, 2)) * 0.125, -1).reshape(b, h, t, t).mean(1)
+    assert got.dtype == torch.float32 and got.shape == (b, t, t)
+    torch.testing.assert_close(got.double(), ref, rtol=2e-5, atol=1e-7)
+    torch.testing.assert_close(got.double().sum(-1), torch.ones((b, t), dtype=torch.float64), rtol=0, atol=2e-5)
