@@ -211,6 +211,44 @@ int musc_attention_weights(const void* q, const void* k, int dtype, int batch, i
                            int t, int d, float scale, float* weights,
                            void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Strided variants: head bh = b*heads + h of q, k, v lives at element
+ * b*in_sb + h*in_sh + row*in_st (+ d); the output at b*out_sb + h*out_sh + row*out_st.
+ * This reads nn.MultiheadAttention's packed in-projection output (t, batch, 3,
+ * heads, 64) in place (q, k, v = base, base + heads*64, base + 2*heads*64;
+ * in_st = batch*3*heads*64, in_sb = 3*heads*64, in_sh = 64) and writes the
+ * (t, batch, heads*64) layout the out-projection takes, so the head transposes of
+ * the reference's math path (torch/nn/functional.py multi_head_attention_forward,
+ * called at models/backbone/open_clip/transformer.py:232-234) are not made.
+ * Strides in elements, >= 0, multiples of 16 bytes; in_st, out_st >= d. */
+int musc_attention_fwd_strided(const void* q, const void* k, const void* v, void* out,
+                               int dtype, int batch, int heads, int t, int d,
+                               long long in_sb, long long in_sh, long long in_st,
+                               long long out_sb, long long out_sh, long long out_st,
+                               float scale, hipStream_t stream);
+int musc_attention_weights_strided(const void* q, const void* k, int dtype, int batch, int heads,
+                                   int t, int d, long long in_sb, long long in_sh, long long in_st,
+                                   float scale, float* weights,
+                                   void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Row LayerNorm over the last dimension `width` of (rows, width) x, dtype
+ * MUSC_DTYPE_F32 or MUSC_DTYPE_F16, fp32 statistics and affine (weight, bias fp32,
+ * either may be NULL for 1 / 0), output y in the input dtype: the cast-back
+ * LayerNorm of models/backbone/open_clip/transformer.py:23-29 (under fp16 autocast:
+ * fp32 layer_norm then .to(fp16)).  With residual != NULL it first forms
+ * sum_out = x + residual rounded to the dtype (the residual add of
+ * transformer.py:247) and normalises that (ln_2 of :248).  sum_out may alias x or
+ * residual.  width % (16 bytes / element size) == 0, width <= 2048 (fp16) / 1024
+ * (fp32); 16-byte aligned buffers. */
+int musc_layernorm_rows(const void* x, const void* residual, void* sum_out,
+                        const float* weight, const float* bias, int dtype, int rows, int width,
+                        float eps, void* y, hipStream_t stream);
+
+#define MUSC_ACT_QUICK_GELU 0  /* x * sigmoid(1.702 x), transformer.py:32-35 (fp16: the
+                                  three torch ops' roundings: 1.702 x, sigmoid, product) */
+#define MUSC_ACT_GELU 1        /* nn.GELU (erf form), model.py:87 for non-OpenAI weights */
+/* y = act(x) elementwise over n values (y may alias x); n a multiple of 16 bytes. */
+int musc_activation(const void* x, void* y, int dtype, int mode, long long n, hipStream_t stream);
+
 /* Calibration (no counterpart in the reference; a measurement aid): `blocks`
  * workgroups of 4 waves each issue iters*64 independent v_mfma_f32_32x32x2f32
  * with no memory traffic, then write one float per thread to out (blocks*256

@@ -30,6 +30,17 @@ constexpr int WAVES = 4;
 constexpr int KPITCH = D + 4;       // K block row pitch (floats)
 constexpr int VPITCH = KB + 4;      // V^T block row pitch (floats)
 
+// Where head bh = b * heads + h of a (batch, heads, t, 64) tensor lives: element
+// (bh, row, d) is at b * sb + h * sh + row * st + d (strides in elements).  The
+// contiguous (batch*heads, t, 64) layout is sb = heads*t*64, sh = t*64, st = 64; the
+// packed in-projection output (t, batch, 3, heads, 64) of nn.MultiheadAttention is
+// read in place with st = batch*3*heads*64, sb = 3*heads*64, sh = 64.
+struct HeadLayout {
+  long long sb, sh, st;
+  int heads;
+  __device__ inline long long base(int bh) const { return (long long)(bh / heads) * sb + (long long)(bh % heads) * sh; }
+};
+
 template <int kDtype>
 __device__ inline float4 ld4(const void* base, long long idx4) {
   if (kDtype == MUSC_DTYPE_F32) return reinterpret_cast<const float4*>(base)[idx4];
@@ -56,10 +67,11 @@ __device__ inline void st4(void* base, long long idx4, float4 v) {
 // (idx = tid + 256*i -> key idx/16, channels 4*(idx%16)) into registers, one block
 // ahead of the compute; the LDS copy is double-buffered so one barrier per block
 // suffices.
-__device__ inline float4 load_kv_row(const float* __restrict__ src, long long head4, int t, int kb, int idx) {
+__device__ inline float4 load_kv_row(const float* __restrict__ src, long long head, long long st, int t, int kb,
+                                     int idx) {
   const int key = idx / (D / 4), d4 = idx % (D / 4);
   const int gk = kb * KB + key;
-  return gk < t ? reinterpret_cast<const float4*>(src)[head4 + (long long)gk * (D / 4) + d4]
+  return gk < t ? *reinterpret_cast<const float4*>(src + head + (long long)gk * st + 4 * d4)
                 : make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
@@ -75,7 +87,8 @@ __device__ inline void store_kv_row(float* __restrict__ Ks, float* __restrict__ 
 __global__ __launch_bounds__(WAVES * kWave, 3) void attn_fwd_kernel(const float* __restrict__ qg,
                                                                  const float* __restrict__ kg,
                                                                  const float* __restrict__ vg,
-                                                                 float* __restrict__ og, int t, float scale_log2) {
+                                                                 float* __restrict__ og, int t, float scale_log2,
+                                                                 HeadLayout in, HeadLayout out) {
   __shared__ __attribute__((aligned(16))) float Ks[2][KB * KPITCH];
   __shared__ __attribute__((aligned(16))) float Vt[2][D * VPITCH];
 
@@ -83,7 +96,7 @@ __global__ __launch_bounds__(WAVES * kWave, 3) void attn_fwd_kernel(const float*
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int lq = lane & 31, lh = lane >> 5;
   const int q = blockIdx.x * (QW * WAVES) + wave * QW + lq;
-  const long long head4 = (long long)bh * t * (D / 4);
+  const long long head = in.base(bh), st = in.st;
 
   // This lane's query row, pre-scaled by scale*log2(e): qr[s][j] = q[8s + 4h + j].
   float qr[8][4];
@@ -91,7 +104,7 @@ __global__ __launch_bounds__(WAVES * kWave, 3) void attn_fwd_kernel(const float*
     const bool ok = q < t;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      float4 v = ok ? reinterpret_cast<const float4*>(qg)[head4 + (long long)q * (D / 4) + 2 * s + lh]
+      float4 v = ok ? *reinterpret_cast<const float4*>(qg + head + (long long)q * st + 8 * s + 4 * lh)
                     : make_float4(0.f, 0.f, 0.f, 0.f);
       qr[s][0] = v.x * scale_log2;
       qr[s][1] = v.y * scale_log2;
@@ -113,17 +126,17 @@ __global__ __launch_bounds__(WAVES * kWave, 3) void attn_fwd_kernel(const float*
   // 32-key block (key idx/16, channels 4*(idx%16)), loaded one block ahead; the LDS
   // copy is double-buffered, so one barrier per block suffices.
   const int i0 = threadIdx.x, i1 = threadIdx.x + WAVES * kWave;
-  float4 k0 = load_kv_row(kg, head4, t, 0, i0), k1 = load_kv_row(kg, head4, t, 0, i1);
-  float4 v0 = load_kv_row(vg, head4, t, 0, i0), v1 = load_kv_row(vg, head4, t, 0, i1);
+  float4 k0 = load_kv_row(kg, head, st, t, 0, i0), k1 = load_kv_row(kg, head, st, t, 0, i1);
+  float4 v0 = load_kv_row(vg, head, st, t, 0, i0), v1 = load_kv_row(vg, head, st, t, 0, i1);
   for (int kb = 0; kb < nkb; ++kb) {
     const int buf = kb & 1;
     store_kv_row(Ks[buf], Vt[buf], i0, k0, v0);
     store_kv_row(Ks[buf], Vt[buf], i1, k1, v1);
     if (kb + 1 < nkb) {
-      k0 = load_kv_row(kg, head4, t, kb + 1, i0);
-      k1 = load_kv_row(kg, head4, t, kb + 1, i1);
-      v0 = load_kv_row(vg, head4, t, kb + 1, i0);
-      v1 = load_kv_row(vg, head4, t, kb + 1, i1);
+      k0 = load_kv_row(kg, head, st, t, kb + 1, i0);
+      k1 = load_kv_row(kg, head, st, t, kb + 1, i1);
+      v0 = load_kv_row(vg, head, st, t, kb + 1, i0);
+      v1 = load_kv_row(vg, head, st, t, kb + 1, i1);
     }
     __syncthreads();
 
@@ -194,8 +207,9 @@ __global__ __launch_bounds__(WAVES * kWave, 3) void attn_fwd_kernel(const float*
     for (int g = 0; g < 4; ++g) {
       const float4 a = make_float4(o0[4 * g] * inv, o0[4 * g + 1] * inv, o0[4 * g + 2] * inv, o0[4 * g + 3] * inv);
       const float4 b = make_float4(o1[4 * g] * inv, o1[4 * g + 1] * inv, o1[4 * g + 2] * inv, o1[4 * g + 3] * inv);
-      reinterpret_cast<float4*>(og)[head4 + (long long)q * (D / 4) + (8 * g + 4 * lh) / 4] = a;
-      reinterpret_cast<float4*>(og)[head4 + (long long)q * (D / 4) + (32 + 8 * g + 4 * lh) / 4] = b;
+      float* orow = og + out.base(bh) + (long long)q * out.st;
+      *reinterpret_cast<float4*>(orow + 8 * g + 4 * lh) = a;
+      *reinterpret_cast<float4*>(orow + 32 + 8 * g + 4 * lh) = b;
     }
   }
 }
@@ -216,7 +230,8 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
                                                                      const _Float16* __restrict__ kg,
                                                                      const _Float16* __restrict__ vg,
                                                                      _Float16* __restrict__ og, int t,
-                                                                     float scale_log2) {
+                                                                     float scale_log2, HeadLayout in,
+                                                                     HeadLayout out) {
   __shared__ __attribute__((aligned(16))) _Float16 Ks[2][KB * KP16];
   __shared__ __attribute__((aligned(16))) _Float16 Vt[2][D * VP16];
 
@@ -224,7 +239,7 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int lq = lane & 31, lh = lane >> 5;
   const int q = blockIdx.x * (QW * WAVES) + wave * QW + lq;
-  const long long head = (long long)bh * t * D;
+  const long long head = in.base(bh), st = in.st;
 
   half8 qf[4];
   {
@@ -232,7 +247,7 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       half8 v = {};
-      if (ok) v = *reinterpret_cast<const half8*>(qg + head + (long long)q * D + 16 * m + 8 * lh);
+      if (ok) v = *reinterpret_cast<const half8*>(qg + head + (long long)q * st + 16 * m + 8 * lh);
 #pragma unroll
       for (int j = 0; j < 8; ++j) v[j] = (_Float16)((float)v[j] * scale_log2);
       qf[m] = v;
@@ -256,13 +271,13 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
   auto load_k = [&](int kb) -> half8 {
     const int gk = kb * KB + skey;
     half8 r = {};
-    if (gk < t) r = *reinterpret_cast<const half8*>(kg + head + (long long)gk * D + sd8);
+    if (gk < t) r = *reinterpret_cast<const half8*>(kg + head + (long long)gk * st + sd8);
     return r;
   };
   auto load_v = [&](int kb, int which) -> half4 {
     const int gk = kb * KB + 2 * kp + which;
     half4 r = {};
-    if (gk < t) r = *reinterpret_cast<const half4*>(vg + head + (long long)gk * D + 4 * dg);
+    if (gk < t) r = *reinterpret_cast<const half4*>(vg + head + (long long)gk * st + 4 * dg);
     return r;
   };
   half8 kreg = load_k(0);
@@ -340,8 +355,9 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
     for (int g = 0; g < 4; ++g) {
       const float4 a = make_float4(o0[4 * g] * inv, o0[4 * g + 1] * inv, o0[4 * g + 2] * inv, o0[4 * g + 3] * inv);
       const float4 b = make_float4(o1[4 * g] * inv, o1[4 * g + 1] * inv, o1[4 * g + 2] * inv, o1[4 * g + 3] * inv);
-      st4<MUSC_DTYPE_F16>(og, (head + (long long)q * D + 8 * g + 4 * lh) / 4, a);
-      st4<MUSC_DTYPE_F16>(og, (head + (long long)q * D + 32 + 8 * g + 4 * lh) / 4, b);
+      const long long orow = out.base(bh) + (long long)q * out.st;
+      st4<MUSC_DTYPE_F16>(og, (orow + 8 * g + 4 * lh) / 4, a);
+      st4<MUSC_DTYPE_F16>(og, (orow + 32 + 8 * g + 4 * lh) / 4, b);
     }
   }
 }
@@ -378,11 +394,11 @@ struct QFrag<MUSC_DTYPE_F32> {
 // half lh: fp16 -> halves 16m + 8lh .. +7 for m = 0..3; fp32 -> floats 8s + 4lh ..
 // +3 for s = 0..7.
 template <int kDtype>
-__device__ inline QFrag<kDtype> load_frag(const void* base, long long head, int row, int t, int lh) {
+__device__ inline QFrag<kDtype> load_frag(const void* base, long long head, long long st, int row, int t, int lh) {
   QFrag<kDtype> f;
   const bool ok = row < t;
   if constexpr (kDtype == MUSC_DTYPE_F16) {
-    const _Float16* p = static_cast<const _Float16*>(base) + head + (long long)row * D + 8 * lh;
+    const _Float16* p = static_cast<const _Float16*>(base) + head + (long long)row * st + 8 * lh;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       half8 v = {};
@@ -390,7 +406,7 @@ __device__ inline QFrag<kDtype> load_frag(const void* base, long long head, int 
       f.v[m] = v;
     }
   } else {
-    const float* p = static_cast<const float*>(base) + head + (long long)row * D + 4 * lh;
+    const float* p = static_cast<const float*>(base) + head + (long long)row * st + 4 * lh;
 #pragma unroll
     for (int s = 0; s < 8; ++s) f.v[s] = ok ? *reinterpret_cast<const float4*>(p + 8 * s) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
@@ -422,18 +438,19 @@ __device__ inline floatx16 logits_t(const QFrag<kDtype>& kf, const QFrag<kDtype>
 // grid (ceil(t/32), batch*heads), one wave.  stats[bh*t + i] = (max, 1/sum).
 template <int kDtype>
 __global__ __launch_bounds__(kWave) void attn_wstats_kernel(const void* __restrict__ qg, const void* __restrict__ kg,
-                                                            int t, float scale_log2, float2* __restrict__ stats) {
+                                                            int t, float scale_log2, HeadLayout in,
+                                                            float2* __restrict__ stats) {
   const int bh = blockIdx.y;
   const int lane = threadIdx.x, lq = lane & 31, lh = lane >> 5;
   const int query = blockIdx.x * 32 + lq;
-  const long long head = (long long)bh * t * D;
-  const QFrag<kDtype> qf = load_frag<kDtype>(qg, head, query, t, lh);
+  const long long head = in.base(bh), st = in.st;
+  const QFrag<kDtype> qf = load_frag<kDtype>(qg, head, st, query, t, lh);
   const int nkb = (t + KB - 1) / KB;
   float m_run = -INFINITY, l_run = 0.f;
-  QFrag<kDtype> kf = load_frag<kDtype>(kg, head, lq, t, lh);
+  QFrag<kDtype> kf = load_frag<kDtype>(kg, head, st, lq, t, lh);
   for (int kb = 0; kb < nkb; ++kb) {
     floatx16 s = logits_t<kDtype>(kf, qf);
-    if (kb + 1 < nkb) kf = load_frag<kDtype>(kg, head, (kb + 1) * KB + lq, t, lh);
+    if (kb + 1 < nkb) kf = load_frag<kDtype>(kg, head, st, (kb + 1) * KB + lq, t, lh);
 #pragma unroll
     for (int v = 0; v < 16; ++v) s[v] *= scale_log2;
     if ((kb + 1) * KB > t) {
@@ -459,7 +476,7 @@ __global__ __launch_bounds__(kWave) void attn_wstats_kernel(const void* __restri
 // grid (ceil(t/32), ceil(nkb/kKR), batch), one wave.
 template <int kDtype, int kKR>
 __global__ __launch_bounds__(kWave) void attn_weights_kernel(const void* __restrict__ qg, const void* __restrict__ kg,
-                                                             int heads, int t, float scale_log2,
+                                                             int heads, int t, float scale_log2, HeadLayout in,
                                                              const float2* __restrict__ stats,
                                                              float* __restrict__ weights) {
   __shared__ float tile[32][33];
@@ -475,8 +492,8 @@ __global__ __launch_bounds__(kWave) void attn_weights_kernel(const void* __restr
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[r][v] = 0.f;
   for (int h = 0; h < heads; ++h) {
-    const long long head = ((long long)b * heads + h) * t * D;
-    const QFrag<kDtype> qf = load_frag<kDtype>(qg, head, query, t, lh);
+    const long long head = in.base(b * heads + h), st = in.st;
+    const QFrag<kDtype> qf = load_frag<kDtype>(qg, head, st, query, t, lh);
     float mx = 0.f, il = 0.f;  // rows past t contribute nothing and are not written
     if (query < t) {
       const float2 st = stats[((long long)b * heads + h) * t + query];
@@ -487,7 +504,7 @@ __global__ __launch_bounds__(kWave) void attn_weights_kernel(const void* __restr
     for (int r = 0; r < kKR; ++r) {
       if (r < nr) {
         const int kb = kb0 + r;
-        const QFrag<kDtype> kf = load_frag<kDtype>(kg, head, kb * KB + lq, t, lh);
+        const QFrag<kDtype> kf = load_frag<kDtype>(kg, head, st, kb * KB + lq, t, lh);
         const floatx16 s = logits_t<kDtype>(kf, qf);
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[r][v] += exp2f(s[v] * scale_log2 - mx) * il;
@@ -520,42 +537,45 @@ __global__ __launch_bounds__(kWave) void attn_weights_kernel(const void* __restr
 
 using namespace musc;
 
-extern "C" int musc_attention_fwd(const void* q, const void* k, const void* v, void* out, int dtype, int bh, int t,
-                                  int d, float scale, hipStream_t stream) {
-  if (!q || !k || !v || !out || bh < 1 || t < 1) return MUSC_ERR_INVALID_ARG;
+namespace {
+
+// Strides must keep every 16-byte vector access aligned and be non-negative.
+inline bool layout_ok(const attn::HeadLayout& l, int dtype) {
+  const long long unit = dtype == MUSC_DTYPE_F32 ? 4 : 8;
+  return l.sb >= 0 && l.sh >= 0 && l.st >= attn::D && l.sb % unit == 0 && l.sh % unit == 0 && l.st % unit == 0;
+}
+
+int attention_fwd(const void* q, const void* k, const void* v, void* out, int dtype, int batch, int heads, int t,
+                  int d, const attn::HeadLayout& in, const attn::HeadLayout& ol, float scale, hipStream_t stream) {
+  if (!q || !k || !v || !out || batch < 1 || heads < 1 || t < 1) return MUSC_ERR_INVALID_ARG;
   if (dtype != MUSC_DTYPE_F32 && dtype != MUSC_DTYPE_F16) return MUSC_ERR_INVALID_ARG;
   if (d != attn::D) return MUSC_ERR_UNSUPPORTED;
-  const uintptr_t align = 16;
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
-       reinterpret_cast<uintptr_t>(out)) % align)
+       reinterpret_cast<uintptr_t>(out)) % 16)
     return MUSC_ERR_INVALID_ARG;
-  if (bh > 65535) return MUSC_ERR_UNSUPPORTED;
+  if (!layout_ok(in, dtype) || !layout_ok(ol, dtype)) return MUSC_ERR_INVALID_ARG;
+  if ((long long)batch * heads > 65535) return MUSC_ERR_UNSUPPORTED;
   const float scale_log2 = scale * 1.4426950408889634f;
-  dim3 grid((t + attn::QW * attn::WAVES - 1) / (attn::QW * attn::WAVES), bh);
+  dim3 grid((t + attn::QW * attn::WAVES - 1) / (attn::QW * attn::WAVES), batch * heads);
   if (dtype == MUSC_DTYPE_F32)
     hipLaunchKernelGGL(attn::attn_fwd_kernel, grid, dim3(attn::WAVES * kWave), 0, stream,
                        static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
-                       static_cast<float*>(out), t, scale_log2);
+                       static_cast<float*>(out), t, scale_log2, in, ol);
   else
     hipLaunchKernelGGL(attn::attn_fwd_f16_kernel, grid, dim3(attn::WAVES * kWave), 0, stream,
                        static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
-                       static_cast<const _Float16*>(v), static_cast<_Float16*>(out), t, scale_log2);
+                       static_cast<const _Float16*>(v), static_cast<_Float16*>(out), t, scale_log2, in, ol);
   return check_launch();
 }
 
-extern "C" int musc_attention_weights_workspace_bytes(int batch, int heads, int t, size_t* out) {
-  if (!out || batch < 1 || heads < 1 || t < 1) return MUSC_ERR_INVALID_ARG;
-  *out = align_up((size_t)batch * heads * t * sizeof(float2), 256);
-  return MUSC_OK;
-}
-
-extern "C" int musc_attention_weights(const void* q, const void* k, int dtype, int batch, int heads, int t, int d,
-                                      float scale, float* weights, void* workspace, size_t workspace_bytes,
-                                      hipStream_t stream) {
+int attention_weights(const void* q, const void* k, int dtype, int batch, int heads, int t, int d,
+                      const attn::HeadLayout& in, float scale, float* weights, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream) {
   if (!q || !k || !weights || batch < 1 || heads < 1 || t < 1) return MUSC_ERR_INVALID_ARG;
   if (dtype != MUSC_DTYPE_F32 && dtype != MUSC_DTYPE_F16) return MUSC_ERR_INVALID_ARG;
   if (d != attn::D) return MUSC_ERR_UNSUPPORTED;
   if (((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k)) % 16) != 0) return MUSC_ERR_INVALID_ARG;
+  if (!layout_ok(in, dtype)) return MUSC_ERR_INVALID_ARG;
   if (batch > 65535 || (long long)batch * heads > 65535) return MUSC_ERR_UNSUPPORTED;
   const size_t need = align_up((size_t)batch * heads * t * sizeof(float2), 256);
   if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) % 8) != 0)
@@ -567,15 +587,60 @@ extern "C" int musc_attention_weights(const void* q, const void* k, int dtype, i
   if (dtype == MUSC_DTYPE_F32) {
     constexpr int kKR = 4;
     hipLaunchKernelGGL(attn::attn_wstats_kernel<MUSC_DTYPE_F32>, sgrid, dim3(kWave), 0, stream, q, k, t, scale_log2,
-                       stats);
+                       in, stats);
     hipLaunchKernelGGL((attn::attn_weights_kernel<MUSC_DTYPE_F32, kKR>), dim3(nqb, (nkb + kKR - 1) / kKR, batch),
-                       dim3(kWave), 0, stream, q, k, heads, t, scale_log2, stats, weights);
+                       dim3(kWave), 0, stream, q, k, heads, t, scale_log2, in, stats, weights);
   } else {
     constexpr int kKR = 8;
     hipLaunchKernelGGL(attn::attn_wstats_kernel<MUSC_DTYPE_F16>, sgrid, dim3(kWave), 0, stream, q, k, t, scale_log2,
-                       stats);
+                       in, stats);
     hipLaunchKernelGGL((attn::attn_weights_kernel<MUSC_DTYPE_F16, kKR>), dim3(nqb, (nkb + kKR - 1) / kKR, batch),
-                       dim3(kWave), 0, stream, q, k, heads, t, scale_log2, stats, weights);
+                       dim3(kWave), 0, stream, q, k, heads, t, scale_log2, in, stats, weights);
   }
   return check_launch();
+}
+
+attn::HeadLayout contiguous(int heads, int t) {
+  return attn::HeadLayout{(long long)heads * t * attn::D, (long long)t * attn::D, attn::D, heads};
+}
+
+}  // namespace
+
+extern "C" int musc_attention_fwd(const void* q, const void* k, const void* v, void* out, int dtype, int bh, int t,
+                                  int d, float scale, hipStream_t stream) {
+  if (bh < 1 || t < 1) return MUSC_ERR_INVALID_ARG;
+  const attn::HeadLayout l = contiguous(1, t);
+  return attention_fwd(q, k, v, out, dtype, bh, 1, t, d, l, l, scale, stream);
+}
+
+extern "C" int musc_attention_fwd_strided(const void* q, const void* k, const void* v, void* out, int dtype,
+                                          int batch, int heads, int t, int d, long long in_sb, long long in_sh,
+                                          long long in_st, long long out_sb, long long out_sh, long long out_st,
+                                          float scale, hipStream_t stream) {
+  if (heads < 1) return MUSC_ERR_INVALID_ARG;
+  return attention_fwd(q, k, v, out, dtype, batch, heads, t, d, attn::HeadLayout{in_sb, in_sh, in_st, heads},
+                       attn::HeadLayout{out_sb, out_sh, out_st, heads}, scale, stream);
+}
+
+extern "C" int musc_attention_weights_workspace_bytes(int batch, int heads, int t, size_t* out) {
+  if (!out || batch < 1 || heads < 1 || t < 1) return MUSC_ERR_INVALID_ARG;
+  *out = align_up((size_t)batch * heads * t * sizeof(float2), 256);
+  return MUSC_OK;
+}
+
+extern "C" int musc_attention_weights(const void* q, const void* k, int dtype, int batch, int heads, int t, int d,
+                                      float scale, float* weights, void* workspace, size_t workspace_bytes,
+                                      hipStream_t stream) {
+  if (batch < 1 || heads < 1 || t < 1) return MUSC_ERR_INVALID_ARG;
+  return attention_weights(q, k, dtype, batch, heads, t, d, contiguous(heads, t), scale, weights, workspace,
+                           workspace_bytes, stream);
+}
+
+extern "C" int musc_attention_weights_strided(const void* q, const void* k, int dtype, int batch, int heads, int t,
+                                              int d, long long in_sb, long long in_sh, long long in_st, float scale,
+                                              float* weights, void* workspace, size_t workspace_bytes,
+                                              hipStream_t stream) {
+  if (heads < 1) return MUSC_ERR_INVALID_ARG;
+  return attention_weights(q, k, dtype, batch, heads, t, d, attn::HeadLayout{in_sb, in_sh, in_st, heads}, scale,
+                           weights, workspace, workspace_bytes, stream);
 }

@@ -1,19 +1,31 @@
-"""Encoding plugin: the encoder with this build's fused attention.
+"""Encoding plugin: the encoder with this build's fused attention and block layers.
 
 Mirrors models/modules/_encoder_gpu.py:45-69 and the accelerated encoder of
 models/modules/_attention_gpu.py:87-157.  The reference patches F.softmax and
 torch.bmm while `model.encode_image` runs, so that nn.MultiheadAttention's math
 path (bmm -> softmax -> bmm over (B*16, 1370, 1370) logits) uses its fused
-softmax.  Here the whole attention of every ViT block is replaced for the
-duration of the call: `attn.forward` of each `nn.MultiheadAttention` in
-`model.visual.transformer.resblocks` computes the input projection, runs
-softmax(q k^T / sqrt(d)) v in one fused kernel (libmusc_hip musc_attention_fwd;
-the (B*H, T, T) logits never exist), then the output projection.  Only block 12,
-whose weights Transformer.forward keeps (transformer.py:331-333), also returns
-head-averaged probabilities (musc_attention_weights); other blocks return None
-for the weights, which their caller discards.  Calls that are not plain
-self-attention (masks, separate key/value, batch_first, d != 64) keep the
-module's own forward.  The original forwards are restored on exit.
+softmax.  Here, for the duration of the call, the forward of every block in
+`model.visual.transformer.resblocks` is replaced:
+
+* block level (ResidualAttentionBlock, transformer.py:236-248, with the cast-back
+  LayerNorm of :23-29 and QuickGELU of :32-35 or erf GELU): ln_1 is one fused
+  LayerNorm pass; the in-projection is torch's GEMM (hipBLASLt); softmax(q k^T /
+  sqrt(d)) v runs in one fused kernel that reads q, k, v straight out of the packed
+  (T, B, 3E) projection and writes the (T, B, E) layout the out-projection takes
+  (libmusc_hip musc_attention_fwd_strided; no logits, no head transposes); the
+  residual add and ln_2 are one pass (musc_layernorm_rows with a residual); c_fc
+  (GEMM with bias) is followed by one in-place activation pass (musc_activation);
+  c_proj and the last residual add are torch.
+* attention level, for blocks of any other structure: only the
+  nn.MultiheadAttention forward is replaced by in-projection -> fused attention ->
+  out-projection.
+
+Only block 12, whose weights Transformer.forward keeps (transformer.py:331-333),
+also returns head-averaged probabilities (musc_attention_weights_strided); other
+blocks return None for the weights, which their caller discards.  Calls that are
+not plain self-attention (masks, separate key/value, batch_first, d != 64,
+gradients) keep the module's own forward.  The original forwards are restored on
+exit.
 
 Hook attributes match the reference: encode_image.aggregate_features,
 encode_image.new_aggregation, encode_image.begin_inference.
@@ -26,7 +38,8 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
-from . import _attention_hip
+from . import _attention_hip, _layers_hip
+from . import _runtime as rt
 from ._aggregation_cache import RadiusAggregationCache
 from ._lnamd_hip import aggregate_features
 
@@ -35,64 +48,144 @@ _STATS = {}
 
 def begin_inference():
     _STATS.clear()
-    _STATS.update(fused_attention_calls=0, weight_blocks=0, fallback_calls=0, seconds=0.0)
+    _STATS.update(fused_blocks=0, fused_attention_calls=0, weight_blocks=0, fallback_calls=0, seconds=0.0)
 
 
-def _fused_forward(attn: nn.MultiheadAttention, original, keep_weights: bool):
+def _count(key: str) -> None:
+    _STATS[key] = _STATS.get(key, 0) + 1
+
+
+def _mha_ok(attn: nn.MultiheadAttention, x: torch.Tensor) -> bool:
+    e, h = attn.embed_dim, attn.num_heads
+    return (not attn.batch_first and attn._qkv_same_embed_dim and attn.in_proj_bias is not None
+            and e % h == 0 and e // h == 64 and x.is_cuda and x.ndim == 3 and x.shape[-1] == e
+            and x.dtype in (torch.float32, torch.float16) and not torch.is_grad_enabled())
+
+
+def _attention(attn: nn.MultiheadAttention, y: torch.Tensor, keep_weights: bool):
+    """Self-attention of nn.MultiheadAttention on (T, B, E) input y: (out, weights | None),
+    or None when the projection's dtype has no kernel."""
+    qkv = F.linear(y, attn.in_proj_weight, attn.in_proj_bias)   # (T, B, 3E), autocast-aware
+    if qkv.dtype not in (torch.float32, torch.float16):
+        return None
+    qkv = qkv.contiguous()
+    h = attn.num_heads
+    scale = 64 ** -0.5
+    o = _attention_hip.attention_packed(qkv, h, scale)                # (T, B, E)
+    weights = _attention_hip.attention_weights_packed(qkv, h, scale) if keep_weights else None
+    _count('fused_attention_calls')
+    if weights is not None:
+        _count('weight_blocks')
+    return F.linear(o, attn.out_proj.weight, attn.out_proj.bias), weights
+
+
+def _fused_mha_forward(attn: nn.MultiheadAttention, original, keep_weights: bool):
     def forward(query, key, value, key_padding_mask=None, need_weights=True, attn_mask=None,
                 average_attn_weights=True, is_causal=False):
-        e = attn.embed_dim
-        h = attn.num_heads
-        ok = (query is key and key is value and key_padding_mask is None and attn_mask is None and not is_causal
-              and not attn.batch_first and attn._qkv_same_embed_dim and attn.in_proj_bias is not None
-              and query.is_cuda and query.ndim == 3 and e // h == 64 and e % h == 0
-              and query.dtype in (torch.float32, torch.float16) and average_attn_weights
-              and not torch.is_grad_enabled())
-        if not ok:
-            _STATS['fallback_calls'] = _STATS.get('fallback_calls', 0) + 1
+        res = None
+        if (query is key and key is value and key_padding_mask is None and attn_mask is None and not is_causal
+                and average_attn_weights and _mha_ok(attn, query)):
+            res = _attention(attn, query, need_weights and keep_weights)
+        if res is None:
+            _count('fallback_calls')
             return original(query, key, value, key_padding_mask=key_padding_mask, need_weights=need_weights,
                             attn_mask=attn_mask, average_attn_weights=average_attn_weights, is_causal=is_causal)
-        t, b, _ = query.shape
-        qkv = F.linear(query, attn.in_proj_weight, attn.in_proj_bias)       # (T, B, 3E), autocast-aware
-        dt = torch.float16 if qkv.dtype == torch.float16 else torch.float32
-        qkv = qkv.to(dt).reshape(t, b, 3, h, 64)                             # [q | k | v], each H x 64
-        q = qkv[:, :, 0].reshape(t, b * h, 64).transpose(0, 1).contiguous()  # (B*H, T, 64), b-major
-        k = qkv[:, :, 1].reshape(t, b * h, 64).transpose(0, 1).contiguous()
-        v = qkv[:, :, 2].reshape(t, b * h, 64).transpose(0, 1).contiguous()
-        scale = 64 ** -0.5
-        out = _attention_hip.attention(q, k, v, scale)                      # (B*H, T, 64)
-        weights = _attention_hip.attention_weights(q, k, h, scale) if (need_weights and keep_weights) else None
-        out = out.transpose(0, 1).reshape(t, b, e)
-        out = F.linear(out, attn.out_proj.weight, attn.out_proj.bias)
-        _STATS['fused_attention_calls'] = _STATS.get('fused_attention_calls', 0) + 1
-        if weights is not None:
-            _STATS['weight_blocks'] = _STATS.get('weight_blocks', 0) + 1
-        return out, weights
+        return res
+    return forward
+
+
+def _cast_back_layer_norm(ln) -> bool:
+    # the reference's LayerNorm / LayerNormFp32 subclasses return the input dtype;
+    # plain nn.LayerNorm under autocast returns fp32 and is left to torch
+    return (isinstance(ln, nn.LayerNorm) and type(ln) is not nn.LayerNorm
+            and type(ln).__name__ in ('LayerNorm', 'LayerNormFp32') and len(ln.normalized_shape) == 1)
+
+
+def _activation_mode(act):
+    if type(act).__name__ == 'QuickGELU':
+        return rt.ACT_QUICK_GELU
+    if isinstance(act, nn.GELU) and act.approximate == 'none':
+        return rt.ACT_GELU
+    return None
+
+
+def _block_plan(block):
+    """Activation mode when `block` has the ResidualAttentionBlock structure this hook
+    fuses (transformer.py:190-248 without LayerScale or cross-attention), else None."""
+    attn = getattr(block, 'attn', None)
+    mlp = getattr(block, 'mlp', None)
+    if not isinstance(attn, nn.MultiheadAttention) or hasattr(block, 'ln_1_kv'):
+        return None
+    if not (_cast_back_layer_norm(getattr(block, 'ln_1', None)) and _cast_back_layer_norm(getattr(block, 'ln_2', None))):
+        return None
+    for name in ('ls_1', 'ls_2'):
+        if not isinstance(getattr(block, name, nn.Identity()), nn.Identity):
+            return None
+    c_fc, act, c_proj = (getattr(mlp, n, None) for n in ('c_fc', 'gelu', 'c_proj'))
+    if not (isinstance(mlp, nn.Sequential) and len(mlp) == 3 and isinstance(c_fc, nn.Linear)
+            and isinstance(c_proj, nn.Linear)):
+        return None
+    return _activation_mode(act)
+
+
+def _fused_block_forward(block, original, mode: int, keep_weights: bool):
+    ln_1, ln_2, attn = block.ln_1, block.ln_2, block.attn
+    c_fc, c_proj = block.mlp.c_fc, block.mlp.c_proj
+
+    def forward(*args, **kwargs):
+        x = args[0] if len(args) == 1 else None
+        extra = {k: v for k, v in kwargs.items() if v is not None}
+        if x is None or extra or not _mha_ok(attn, x) or not _layers_hip.supports_layer_norm(x.shape[-1], x.dtype):
+            _count('fallback_calls')
+            return original(*args, **kwargs)
+        y = _layers_hip.layer_norm(x, ln_1.weight, ln_1.bias, ln_1.eps)
+        res = _attention(attn, y, keep_weights)
+        if res is None:
+            _count('fallback_calls')
+            return original(*args, **kwargs)
+        a, weights = res
+        if a.dtype == x.dtype:
+            x, y = _layers_hip.layer_norm(x, ln_2.weight, ln_2.bias, ln_2.eps, residual=a)
+        else:
+            x = x + a
+            y = ln_2(x)
+        hdn = F.linear(y, c_fc.weight, c_fc.bias)
+        if hdn.dtype in (torch.float32, torch.float16) and hdn.is_contiguous():
+            _layers_hip.activation_(hdn, mode)
+        else:
+            hdn = block.mlp.gelu(hdn)
+        x = x + F.linear(hdn, c_proj.weight, c_proj.bias)
+        _count('fused_blocks')
+        return x, weights
     return forward
 
 
 def encode_image(model, image, out_layers):
-    """(pooled (B, D), [tokens (B, T, width)] for out_layers) with the fused attention."""
+    """(pooled (B, D), [tokens (B, T, width)] for out_layers) with the fused blocks."""
     blocks = getattr(getattr(getattr(model, 'visual', None), 'transformer', None), 'resblocks', [])
     restored = []
     start = time.perf_counter()
     try:
         for index, block in enumerate(blocks):
-            attention = getattr(block, 'attn', None)
-            if not isinstance(attention, nn.MultiheadAttention):
-                continue
-            present = 'forward' in attention.__dict__
-            previous = attention.__dict__.get('forward')
             keep = (index == 11) or (len(blocks) < 12 and index == len(blocks) - 1)
-            attention.forward = _fused_forward(attention, attention.forward, keep)
-            restored.append((attention, present, previous))
+            mode = _block_plan(block)
+            if mode is not None:
+                target, make = block, (lambda o, b=block, m=mode, k=keep: _fused_block_forward(b, o, m, k))
+            elif isinstance(getattr(block, 'attn', None), nn.MultiheadAttention):
+                target, make = block.attn, (lambda o, a=block.attn, k=keep: _fused_mha_forward(a, o, k))
+            else:
+                continue
+            present = 'forward' in target.__dict__
+            previous = target.__dict__.get('forward')
+            target.forward = make(target.forward)
+            restored.append((target, present, previous))
         return model.encode_image(image, out_layers)
     finally:
-        for attention, present, previous in reversed(restored):
+        for target, present, previous in reversed(restored):
             if present:
-                attention.forward = previous
+                target.forward = previous
             else:
-                attention.__dict__.pop('forward', None)
+                target.__dict__.pop('forward', None)
         _STATS['seconds'] = _STATS.get('seconds', 0.0) + time.perf_counter() - start
 
 

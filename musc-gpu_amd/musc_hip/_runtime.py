@@ -30,6 +30,8 @@ MUSC_ERR_UNSUPPORTED = 1003
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
+ACT_QUICK_GELU = 0
+ACT_GELU = 1
 LAYOUT_RBPLC = 0
 LAYOUT_RLBPC = 1
 LNAMD_L2NORM = 1
@@ -38,7 +40,7 @@ LNAMD_RAW_SUMS = 4
 MSM_NORMALIZE_ROWS = 1
 
 # Every symbol include/musc_hip.h declares, with its ctypes signature.
-_vp, _i, _f, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+_vp, _i, _f, _sz, _ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_longlong
 SIGNATURES = {
     'musc_strerror': (ctypes.c_char_p, [_i]),
     'musc_version': (_i, []),
@@ -56,6 +58,10 @@ SIGNATURES = {
     'musc_attention_fwd': (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp]),
     'musc_attention_weights_workspace_bytes': (_i, [_i, _i, _i, ctypes.POINTER(_sz)]),
     'musc_attention_weights': (_i, [_vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _vp, _sz, _vp]),
+    'musc_attention_fwd_strided': (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _ll, _ll, _ll, _ll, _ll, _ll, _f, _vp]),
+    'musc_attention_weights_strided': (_i, [_vp, _vp, _i, _i, _i, _i, _i, _ll, _ll, _ll, _f, _vp, _vp, _sz, _vp]),
+    'musc_layernorm_rows': (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _vp]),
+    'musc_activation': (_i, [_vp, _vp, _i, _i, _ll, _vp]),
     'musc_calibrate_mfma_f32': (_i, [_vp, _i, _i, ctypes.POINTER(ctypes.c_double), _vp]),
 }
 

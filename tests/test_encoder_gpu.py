@@ -26,10 +26,11 @@ def test_fp32_tokens_match_math_path(device):
     for a, b in zip(tokens, ref_tokens):
         torch.testing.assert_close(a, b, rtol=1e-4, atol=1e-5)
     stats = _encoder_hip.research_diagnostics()
-    assert stats['fused_attention_calls'] == 4 and stats['weight_blocks'] == 1
+    assert stats['fused_blocks'] == 4 and stats['fused_attention_calls'] == 4 and stats['weight_blocks'] == 1
+    assert stats['fallback_calls'] == 0
     # the original forwards are restored
     for blk in model.visual.transformer.resblocks:
-        assert 'forward' not in blk.attn.__dict__
+        assert 'forward' not in blk.__dict__ and 'forward' not in blk.attn.__dict__
 
 
 def test_autocast_fp16(device):
@@ -40,6 +41,58 @@ def test_autocast_fp16(device):
         pooled, tokens = _encoder_hip.encode_image(model, image, [4])
     assert tokens[0].dtype == torch.float16
     torch.testing.assert_close(tokens[0].float(), ref_tokens[0].float(), rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(pooled.float(), ref_pooled.float(), rtol=2e-2, atol=2e-2)
+
+
+def test_attention_level_hook_for_other_blocks(device):
+    # a block whose activation the fused block path does not cover (tanh GELU) keeps its
+    # own forward; only its nn.MultiheadAttention is replaced
+    model = small_model(device, layers=2)
+    for blk in model.visual.transformer.resblocks:
+        blk.mlp.gelu = torch.nn.GELU(approximate='tanh')
+    image = torch.rand((2, 3, 56, 56), generator=torch.Generator().manual_seed(7)).to(device)
+    with torch.no_grad():
+        ref_pooled, ref_tokens = model.encode_image(image, [2])
+        _encoder_hip.begin_inference()
+        pooled, tokens = _encoder_hip.encode_image(model, image, [2])
+    torch.testing.assert_close(tokens[0], ref_tokens[0], rtol=1e-4, atol=1e-5)
+    stats = _encoder_hip.research_diagnostics()
+    assert stats['fused_blocks'] == 0 and stats['fused_attention_calls'] == 2
+    for blk in model.visual.transformer.resblocks:
+        assert 'forward' not in blk.__dict__ and 'forward' not in blk.attn.__dict__
+
+
+def test_masked_call_falls_back(device):
+    model = small_model(device, layers=1)
+    blk = model.visual.transformer.resblocks[0]
+    x = torch.randn((17, 2, 128), generator=torch.Generator().manual_seed(8)).to(device)
+    mask = torch.zeros((17, 17), device=device)
+    mask[:, 3] = float('-inf')
+    with torch.no_grad():
+        ref, _ = blk(x, attn_mask=mask)
+        fused = _encoder_hip._fused_block_forward(blk, blk.forward, 0, False)
+        _encoder_hip.begin_inference()
+        got, _ = fused(x, attn_mask=mask)
+    torch.testing.assert_close(got, ref, rtol=0, atol=0)
+    assert _encoder_hip.research_diagnostics()['fallback_calls'] == 1
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float16])
+def test_packed_attention_matches_contiguous(device, dtype):
+    # the strided kernels read (T, B, 3E) in place; same arithmetic as the contiguous entry
+    g = torch.Generator().manual_seed(9)
+    t, b, h = 300, 3, 4
+    e = 64 * h
+    qkv = (torch.randn((t, b, 3 * e), generator=g) * 0.5).to(dtype).to(device)
+    parts = qkv.reshape(t, b, 3, h, 64)
+    q, k, v = (parts[:, :, i].reshape(t, b * h, 64).transpose(0, 1).contiguous() for i in range(3))
+    ref = _attention_hip.attention(q, k, v, 0.125).transpose(0, 1).reshape(t, b, e)
+    got = _attention_hip.attention_packed(qkv, h, 0.125)
+    assert got.shape == (t, b, e) and got.dtype == dtype
+    assert torch.equal(got, ref)
+    w_ref = _attention_hip.attention_weights(q, k, h, 0.125)
+    w_got = _attention_hip.attention_weights_packed(qkv, h, 0.125)
+    assert torch.equal(w_got, w_ref)
 
 
 def test_vit_l14_full_size_block_tokens(device):
