@@ -151,6 +151,19 @@ int musc_lnamd_f32(const void* const* tokens, int n_layers, int in_dtype,
                    float* out, int out_layout,
                    void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* musc_lnamd_f32 with the side x side grid of outputs adaptively average-pooled to
+ * pool_side x pool_side in the same pass (F.adaptive_avg_pool2d windows, the
+ * super_fast 37 -> 28 step of models/modules/_super_fast.py:17-27 applied after
+ * LNAMD): out holds pool_side^2 patches per (radius, image, layer) in out_layout.
+ * 1 <= pool_side <= side (pool_side == side: no pooling); not with
+ * MUSC_LNAMD_L2NORM.  With MUSC_LNAMD_RAW_SUMS the pooled values are plain sums
+ * (no 1/r^2, no division by the window count: scales an L2-normalising consumer
+ * removes); otherwise LayerNorm + box mean + adaptive mean exactly. */
+int musc_lnamd_pooled_f32(const void* const* tokens, int n_layers, int in_dtype, int batch,
+                          int tokens_per_image, int c, int has_cls, const int* radii, int n_radii,
+                          float eps, int flags, int pool_side, float* out, int out_layout,
+                          void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* Adaptive average pooling of patch grids, F.adaptive_avg_pool2d semantics:
  *   in   (batch, side_in*side_in, ch) fp32, out (batch, side_out*side_out, ch) fp32.
  * The super_fast aggregation pools the r=3 LNAMD grid 37x37 -> 28x28

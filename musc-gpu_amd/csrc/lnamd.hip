@@ -325,13 +325,22 @@ __global__ __launch_bounds__(kMaxThreads) void lnamd_pool_kernel(TokenPtrs token
 //   raw = 0: out = window sum * rstd / r^2   (avg_pool2d of the LayerNorm output)
 //   raw = 1: out = window sum of (x - mean)  (unscaled; for consumers that
 //            L2-normalise, where the scale cancels)
-template <int kDtype, int kHalo, int kNR>
+// kPool: the side x side grid of window sums is adaptively average-pooled to
+// pool x pool (F.adaptive_avg_pool2d windows: rows floor(i*side/pool) ..
+// ceil((i+1)*side/pool) - 1, likewise columns; the super_fast 37 -> 28 step,
+// models/modules/_super_fast.py:17-27) before it is written.  Each finished row of
+// window sums goes to LDS, output-column threads sum their columns, and the row
+// sums accumulate in two register slots (a source row lies in at most two output
+// windows when pool <= side); an output row is written when its last source row
+// is done.  raw = 0 divides by r^2 and the window count, raw = 1 writes the plain
+// sums.
+template <int kDtype, int kHalo, int kNR, bool kPool>
 __global__ __launch_bounds__(1024) void lnamd_stream_kernel(TokenPtrs tokens, int n_layers, int batch,
                                                             int tokens_per_image, int c, int has_cls, int side,
                                                             int cg, int slices, Radii radii, Radii slot, int raw,
-                                                            int layout, const double* __restrict__ stats,
+                                                            int layout, int pool, const double* __restrict__ stats,
                                                             float* __restrict__ out) {
-  extern __shared__ float4 vsum[];  // [2][kNR][side * cg]
+  extern __shared__ float4 vsum[];  // [2][kNR][side * cg], then (kPool) hsum [kNR][side * cg]
   const int unit = blockIdx.x / slices, slice = blockIdx.x % slices;
   const int b = unit / n_layers, l = unit % n_layers;
   const int w = threadIdx.x / cg, gl = threadIdx.x % cg;
@@ -342,8 +351,14 @@ __global__ __launch_bounds__(1024) void lnamd_stream_kernel(TokenPtrs tokens, in
   const void* base = tokens.p[l];
   const float mean = (float)stats[unit * 2 + 0];
   const float rstd = (float)stats[unit * 2 + 1];
-  const int P = side * side;
+  const int P = kPool ? pool * pool : side * side;
   const int row_len = side * cg;
+  float4* hsum = vsum + (size_t)2 * kNR * row_len;
+  // pooled-row accumulators of even and odd output rows (named, not indexed by a
+  // runtime slot, so they stay in registers)
+  float4 pacc_even[kNR], pacc_odd[kNR];
+#pragma unroll
+  for (int k = 0; k < kNR; ++k) pacc_even[k] = pacc_odd[k] = make_float4(0.f, 0.f, 0.f, 0.f);
   const long long col_base4 = (((long long)b * tokens_per_image + has_cls) * c) / 4 + (long long)wl * (c / 4) + gg;
   const long long row_step4 = (long long)side * (c / 4);
 
@@ -396,30 +411,78 @@ __global__ __launch_bounds__(1024) void lnamd_stream_kernel(TokenPtrs tokens, in
             if (w + a < side) acc = f4add(acc, buf[k * row_len + threadIdx.x + a * cg]);
           }
         }
-        const float sc = raw ? 1.f : rstd / (float)(radii.r[k] * radii.r[k]);
-        const int ko = slot.r[k];
-        long long o;
-        if (layout == MUSC_LAYOUT_RBPLC)
-          o = ((((long long)ko * batch + b) * P + p) * n_layers + l) * c;
-        else
-          o = ((((long long)ko * n_layers + l) * batch + b) * P + p) * c;
-        // streaming store: the pools are read back only by later kernels
-        const float4 r = f4scale(acc, sc);
-        const nt_float4 v = {r.x, r.y, r.z, r.w};
-        __builtin_nontemporal_store(v, reinterpret_cast<nt_float4*>(out + o) + g);
+        if constexpr (kPool) {
+          hsum[k * row_len + threadIdx.x] = acc;
+        } else {
+          const float sc = raw ? 1.f : rstd / (float)(radii.r[k] * radii.r[k]);
+          const int ko = slot.r[k];
+          long long o;
+          if (layout == MUSC_LAYOUT_RBPLC)
+            o = ((((long long)ko * batch + b) * P + p) * n_layers + l) * c;
+          else
+            o = ((((long long)ko * n_layers + l) * batch + b) * P + p) * c;
+          // streaming store: the pools are read back only by later kernels
+          const float4 r = f4scale(acc, sc);
+          const nt_float4 v = {r.x, r.y, r.z, r.w};
+          __builtin_nontemporal_store(v, reinterpret_cast<nt_float4*>(out + o) + g);
+        }
+      }
+    }
+    if constexpr (kPool) {
+      __syncthreads();
+      // thread (w, gl) is output column w for the pooling step
+      if (w < pool && g < groups) {
+        const int x0 = (w * side) / pool, x1 = ((w + 1) * side + pool - 1) / pool;
+        float4 hp[kNR];
+#pragma unroll
+        for (int k = 0; k < kNR; ++k) {
+          float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+          for (int x = x0; x < x1; ++x) a = f4add(a, hsum[k * row_len + x * cg + gl]);
+          hp[k] = a;
+        }
+        const int oy0 = (h * pool) / side;  // first output row whose window holds row h
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          const int oy = oy0 + d;
+          if (oy >= pool) continue;
+          const int y0 = (oy * side) / pool, y1 = ((oy + 1) * side + pool - 1) / pool;
+          if (h < y0 || h >= y1) continue;
+          auto add_emit = [&](float4 (&pa)[kNR]) {
+#pragma unroll
+            for (int k = 0; k < kNR; ++k) pa[k] = f4add(pa[k], hp[k]);
+            if (h != y1 - 1) return;
+            const int po = oy * pool + w;
+            const float cnt = (float)((y1 - y0) * (x1 - x0));
+#pragma unroll
+            for (int k = 0; k < kNR; ++k) {
+              const float sc = raw ? 1.f : rstd / ((float)(radii.r[k] * radii.r[k]) * cnt);
+              const int ko = slot.r[k];
+              long long o;
+              if (layout == MUSC_LAYOUT_RBPLC)
+                o = ((((long long)ko * batch + b) * P + po) * n_layers + l) * c;
+              else
+                o = ((((long long)ko * n_layers + l) * batch + b) * P + po) * c;
+              const float4 r = f4scale(pa[k], sc);
+              const nt_float4 v = {r.x, r.y, r.z, r.w};
+              __builtin_nontemporal_store(v, reinterpret_cast<nt_float4*>(out + o) + g);
+              pa[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+          };
+          if (oy & 1) add_emit(pacc_odd); else add_emit(pacc_even);
+        }
       }
     }
   }
 }
 
-template <int kDtype, int kHalo>
+template <int kDtype, int kHalo, bool kPool>
 int dispatch_stream_nr(int nr, dim3 grid, dim3 block, size_t smem, hipStream_t s, const TokenPtrs& tp, int n_layers,
                        int batch, int tpi, int c, int has_cls, int side, int cg, int slices, const Radii& radii,
-                       const Radii& slot, int raw, int layout, const double* stats, float* out) {
+                       const Radii& slot, int raw, int layout, int pool, const double* stats, float* out) {
 #define MUSC_STREAM_CASE(NR)                                                                                      \
   case NR:                                                                                                        \
-    hipLaunchKernelGGL((lnamd_stream_kernel<kDtype, kHalo, NR>), grid, block, smem, s, tp, n_layers, batch, tpi, c, \
-                       has_cls, side, cg, slices, radii, slot, raw, layout, stats, out);                          \
+    hipLaunchKernelGGL((lnamd_stream_kernel<kDtype, kHalo, NR, kPool>), grid, block, smem, s, tp, n_layers, batch, \
+                       tpi, c, has_cls, side, cg, slices, radii, slot, raw, layout, pool, stats, out);            \
     break;
   switch (nr) {
     MUSC_STREAM_CASE(1)
@@ -432,18 +495,24 @@ int dispatch_stream_nr(int nr, dim3 grid, dim3 block, size_t smem, hipStream_t s
   return MUSC_OK;
 }
 
-template <int kDtype>
+template <int kDtype, bool kPool>
 int dispatch_stream(int halo, int nr, dim3 grid, dim3 block, size_t smem, hipStream_t s, const TokenPtrs& tp,
                     int n_layers, int batch, int tpi, int c, int has_cls, int side, int cg, int slices,
-                    const Radii& radii, const Radii& slot, int raw, int layout, const double* stats, float* out) {
+                    const Radii& radii, const Radii& slot, int raw, int layout, int pool, const double* stats,
+                    float* out) {
+#define MUSC_STREAM_HALO(H)                                                                                      \
+  case H:                                                                                                        \
+    return dispatch_stream_nr<kDtype, H, kPool>(nr, grid, block, smem, s, tp, n_layers, batch, tpi, c, has_cls,   \
+                                                side, cg, slices, radii, slot, raw, layout, pool, stats, out);
   switch (halo) {
-    case 0: return dispatch_stream_nr<kDtype, 0>(nr, grid, block, smem, s, tp, n_layers, batch, tpi, c, has_cls, side, cg, slices, radii, slot, raw, layout, stats, out);
-    case 1: return dispatch_stream_nr<kDtype, 1>(nr, grid, block, smem, s, tp, n_layers, batch, tpi, c, has_cls, side, cg, slices, radii, slot, raw, layout, stats, out);
-    case 2: return dispatch_stream_nr<kDtype, 2>(nr, grid, block, smem, s, tp, n_layers, batch, tpi, c, has_cls, side, cg, slices, radii, slot, raw, layout, stats, out);
-    case 3: return dispatch_stream_nr<kDtype, 3>(nr, grid, block, smem, s, tp, n_layers, batch, tpi, c, has_cls, side, cg, slices, radii, slot, raw, layout, stats, out);
-    case 4: return dispatch_stream_nr<kDtype, 4>(nr, grid, block, smem, s, tp, n_layers, batch, tpi, c, has_cls, side, cg, slices, radii, slot, raw, layout, stats, out);
+    MUSC_STREAM_HALO(0)
+    MUSC_STREAM_HALO(1)
+    MUSC_STREAM_HALO(2)
+    MUSC_STREAM_HALO(3)
+    MUSC_STREAM_HALO(4)
     default: return MUSC_ERR_UNSUPPORTED;
   }
+#undef MUSC_STREAM_HALO
 }
 
 // Adaptive average pooling of a side_in x side_in patch grid to side_out x
@@ -528,10 +597,12 @@ extern "C" int musc_lnamd_workspace_bytes(int batch, int n_layers, size_t* out) 
   return MUSC_OK;
 }
 
-extern "C" int musc_lnamd_f32(const void* const* tokens, int n_layers, int in_dtype, int batch,
-                              int tokens_per_image, int c, int has_cls, const int* radii, int n_radii, float eps,
-                              int flags, float* out, int out_layout, void* workspace, size_t workspace_bytes,
-                              hipStream_t stream) {
+namespace {
+
+// pool_side == 0: no pooling (output grid = input grid).
+int lnamd_run(const void* const* tokens, int n_layers, int in_dtype, int batch, int tokens_per_image, int c,
+              int has_cls, const int* radii, int n_radii, float eps, int flags, int pool_side, float* out,
+              int out_layout, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   using namespace lnamd;
   if (!tokens || !radii || !out || n_layers < 1 || batch < 1 || c < 4 || n_radii < 1) return MUSC_ERR_INVALID_ARG;
   if (has_cls != 0 && has_cls != 1) return MUSC_ERR_INVALID_ARG;
@@ -545,6 +616,9 @@ extern "C" int musc_lnamd_f32(const void* const* tokens, int n_layers, int in_dt
   int side = 0;
   while ((side + 1) * (side + 1) <= grid_tokens) ++side;
   if (grid_tokens < 1 || side * side != grid_tokens) return MUSC_ERR_INVALID_ARG;
+  if (pool_side < 0 || pool_side > side) return MUSC_ERR_INVALID_ARG;
+  const bool pooled = pool_side > 0 && pool_side < side;
+  if (pooled && (flags & MUSC_LNAMD_L2NORM)) return MUSC_ERR_UNSUPPORTED;
   Radii rr{};
   rr.n = n_radii;
   int halo = 0;
@@ -608,27 +682,55 @@ extern "C" int musc_lnamd_f32(const void* const* tokens, int n_layers, int in_dt
   } else {
     // streaming kernel: cg channel groups per workgroup, side*cg <= 1024 threads
     const int groups = c / 4;
+    // LDS: double-buffered vertical sums, plus (pooled) one row of window sums
+    const size_t bufs = pooled ? 3 : 2;
     int cg = 1;
     while (cg * 2 <= 16 && cg * 2 <= groups && side * cg * 2 <= 1024 &&
-           (size_t)2 * n_radii * side * cg * 2 * sizeof(float4) <= 64 * 1024)
+           bufs * n_radii * side * cg * 2 * sizeof(float4) <= 64 * 1024)
       cg *= 2;
-    const size_t smem = (size_t)2 * n_radii * side * cg * sizeof(float4);
+    const size_t smem = bufs * n_radii * side * cg * sizeof(float4);
     if (side * cg > 1024 || smem > 64 * 1024) return MUSC_ERR_UNSUPPORTED;
     const int slices = (groups + cg - 1) / cg;
     const int threads = side * cg;
     const int raw = (flags & MUSC_LNAMD_RAW_SUMS) ? 1 : 0;
     const dim3 grid((unsigned)(units * slices));
+    const int pool = pooled ? pool_side : side;
     if (in_dtype == MUSC_DTYPE_F32)
-      rc = dispatch_stream<MUSC_DTYPE_F32>(halo, n_radii, grid, dim3(threads), smem, stream, tp, n_layers, batch,
-                                           tokens_per_image, c, has_cls, side, cg, slices, rr, slot, raw,
-                                           out_layout, stats, out);
+      rc = pooled ? dispatch_stream<MUSC_DTYPE_F32, true>(halo, n_radii, grid, dim3(threads), smem, stream, tp,
+                                                         n_layers, batch, tokens_per_image, c, has_cls, side, cg,
+                                                         slices, rr, slot, raw, out_layout, pool, stats, out)
+                  : dispatch_stream<MUSC_DTYPE_F32, false>(halo, n_radii, grid, dim3(threads), smem, stream, tp,
+                                                          n_layers, batch, tokens_per_image, c, has_cls, side, cg,
+                                                          slices, rr, slot, raw, out_layout, pool, stats, out);
     else
-      rc = dispatch_stream<MUSC_DTYPE_F16>(halo, n_radii, grid, dim3(threads), smem, stream, tp, n_layers, batch,
-                                           tokens_per_image, c, has_cls, side, cg, slices, rr, slot, raw,
-                                           out_layout, stats, out);
+      rc = pooled ? dispatch_stream<MUSC_DTYPE_F16, true>(halo, n_radii, grid, dim3(threads), smem, stream, tp,
+                                                         n_layers, batch, tokens_per_image, c, has_cls, side, cg,
+                                                         slices, rr, slot, raw, out_layout, pool, stats, out)
+                  : dispatch_stream<MUSC_DTYPE_F16, false>(halo, n_radii, grid, dim3(threads), smem, stream, tp,
+                                                          n_layers, batch, tokens_per_image, c, has_cls, side, cg,
+                                                          slices, rr, slot, raw, out_layout, pool, stats, out);
   }
   if (rc) return rc;
   return check_launch();
+}
+
+}  // namespace
+
+extern "C" int musc_lnamd_f32(const void* const* tokens, int n_layers, int in_dtype, int batch,
+                              int tokens_per_image, int c, int has_cls, const int* radii, int n_radii, float eps,
+                              int flags, float* out, int out_layout, void* workspace, size_t workspace_bytes,
+                              hipStream_t stream) {
+  return lnamd_run(tokens, n_layers, in_dtype, batch, tokens_per_image, c, has_cls, radii, n_radii, eps, flags, 0,
+                   out, out_layout, workspace, workspace_bytes, stream);
+}
+
+extern "C" int musc_lnamd_pooled_f32(const void* const* tokens, int n_layers, int in_dtype, int batch,
+                                     int tokens_per_image, int c, int has_cls, const int* radii, int n_radii,
+                                     float eps, int flags, int pool_side, float* out, int out_layout,
+                                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (pool_side < 1) return MUSC_ERR_INVALID_ARG;
+  return lnamd_run(tokens, n_layers, in_dtype, batch, tokens_per_image, c, has_cls, radii, n_radii, eps, flags,
+                   pool_side, out, out_layout, workspace, workspace_bytes, stream);
 }
 
 extern "C" int musc_adaptive_pool_f32(const float* in, int batch, int side_in, int ch, int side_out, float* out,

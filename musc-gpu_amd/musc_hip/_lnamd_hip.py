@@ -47,7 +47,7 @@ def _check_tokens(tokens: list[torch.Tensor]) -> tuple[int, int, int, torch.dtyp
 
 def lnamd(tokens: list[torch.Tensor], radii: list[int], *, l2norm: bool = False, layout: str = 'rbplc',
           has_cls: bool = True, eps: float = 1e-5, stats_workspace: torch.Tensor | None = None,
-          stats_ready: bool = False, raw_sums: bool = False) -> torch.Tensor:
+          stats_ready: bool = False, raw_sums: bool = False, pool_side: int | None = None) -> torch.Tensor:
     """LayerNorm over (C, H, W) + r x r zero-padded box mean for every radius.
 
     tokens  list of L tensors (B, T, C) (T = 1 + side*side when has_cls).
@@ -59,6 +59,10 @@ def lnamd(tokens: list[torch.Tensor], radii: list[int], *, l2norm: bool = False,
              the 1/r^2 (the input of an L2-normalising consumer, where they cancel).
     stats_workspace / stats_ready  reuse LayerNorm statistics computed by an
              earlier call on the same tokens (another radius).
+    pool_side  adaptively average-pool the side x side grid of outputs to
+             pool_side x pool_side in the same pass (F.adaptive_avg_pool2d windows;
+             the super_fast 37 -> 28 step); P becomes pool_side**2.  With raw_sums
+             the pooled values are plain sums (no division by the window count).
     """
     b, t, c, dtype = _check_tokens(tokens)
     side = math.isqrt(t - int(has_cls))
@@ -66,7 +70,11 @@ def lnamd(tokens: list[torch.Tensor], radii: list[int], *, l2norm: bool = False,
         raise ValueError('token count must be a square grid (plus the class token)')
     radii = [int(r) for r in radii]
     n_layers = len(tokens)
-    p = side * side
+    if pool_side is not None and not (1 <= int(pool_side) <= side):
+        raise ValueError(f'pool_side must lie in [1, {side}]')
+    if pool_side is not None and l2norm and int(pool_side) != side:
+        raise ValueError('pooling and the fused L2 normalisation cannot be combined')
+    p = side * side if pool_side is None else int(pool_side) ** 2
     dev = tokens[0].device
     shape = (len(radii), b, p, n_layers, c) if layout == 'rbplc' else (len(radii), n_layers, b, p, c)
     toks = [x.contiguous() for x in tokens]
@@ -80,12 +88,19 @@ def lnamd(tokens: list[torch.Tensor], radii: list[int], *, l2norm: bool = False,
         rad = (ctypes.c_int * len(radii))(*radii)
         flags = ((rt.LNAMD_L2NORM if l2norm else 0) | (rt.LNAMD_STATS_READY if stats_ready else 0)
                  | (rt.LNAMD_RAW_SUMS if raw_sums else 0))
-        rc = rt.library().musc_lnamd_f32(ctypes.cast(ptrs, ctypes.c_void_p), n_layers,
-                                         rt.DTYPE_F32 if dtype == torch.float32 else rt.DTYPE_F16,
-                                         b, t, c, int(has_cls), ctypes.cast(rad, ctypes.c_void_p), len(radii),
-                                         float(eps), flags, out.data_ptr(), _LAYOUTS[layout], ws.data_ptr(),
-                                         ws.numel(), rt.stream(dev))
-        rt.check(rc, 'musc_lnamd_f32')
+        in_dtype = rt.DTYPE_F32 if dtype == torch.float32 else rt.DTYPE_F16
+        if pool_side is None:
+            rc = rt.library().musc_lnamd_f32(ctypes.cast(ptrs, ctypes.c_void_p), n_layers, in_dtype,
+                                             b, t, c, int(has_cls), ctypes.cast(rad, ctypes.c_void_p), len(radii),
+                                             float(eps), flags, out.data_ptr(), _LAYOUTS[layout], ws.data_ptr(),
+                                             ws.numel(), rt.stream(dev))
+            rt.check(rc, 'musc_lnamd_f32')
+        else:
+            rc = rt.library().musc_lnamd_pooled_f32(ctypes.cast(ptrs, ctypes.c_void_p), n_layers, in_dtype,
+                                                    b, t, c, int(has_cls), ctypes.cast(rad, ctypes.c_void_p),
+                                                    len(radii), float(eps), flags, int(pool_side), out.data_ptr(),
+                                                    _LAYOUTS[layout], ws.data_ptr(), ws.numel(), rt.stream(dev))
+            rt.check(rc, 'musc_lnamd_pooled_f32')
     return out
 
 

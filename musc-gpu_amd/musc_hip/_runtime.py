@@ -52,6 +52,7 @@ SIGNATURES = {
     'musc_msm_rank_f32': (_i, [_i, _i, _i, _i, _vp, _vp, _sz, _vp]),
     'musc_lnamd_workspace_bytes': (_i, [_i, _i, ctypes.POINTER(_sz)]),
     'musc_lnamd_f32': (_i, [_vp, _i, _i, _i, _i, _i, _i, _vp, _i, _f, _i, _vp, _i, _vp, _sz, _vp]),
+    'musc_lnamd_pooled_f32': (_i, [_vp, _i, _i, _i, _i, _i, _i, _vp, _i, _f, _i, _i, _vp, _i, _vp, _sz, _vp]),
     'musc_maps_f64': (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp]),
     'musc_adaptive_pool_f32': (_i, [_vp, _i, _i, _i, _i, _vp, _vp]),
     'musc_rscin_f32': (_i, [_vp, _vp, _i, _i, _vp, _i, _vp, _vp]),

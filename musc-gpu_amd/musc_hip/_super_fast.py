@@ -3,7 +3,10 @@
 Mirrors models/modules/_super_fast.py:7-40: `SuperFastAggregation` wraps the
 per-division aggregation, checks its one-layer/r=3/37x37 contract (ValueError
 otherwise) and adaptively average-pools the grid to PATCH_GRID x PATCH_GRID in
-fp32 (libmusc_hip musc_adaptive_pool_f32), returning the features' dtype.
+fp32, returning the features' dtype.  With this package's own aggregation and
+tokens the LNAMD kernel supports, LNAMD and the pooling are one pass
+(musc_lnamd_pooled_f32); otherwise the wrapped aggregation runs and its output is
+pooled by musc_adaptive_pool_f32.
 """
 from __future__ import annotations
 
@@ -11,6 +14,7 @@ import math
 
 import torch
 
+from . import _lnamd_hip
 from . import _runtime as rt
 from ._aggregation_cache import RadiusAggregationCache
 
@@ -44,6 +48,12 @@ class SuperFastAggregation:
         self.base.clear()
 
     def __call__(self, layer, tokens, return_cpu=True):
+        if isinstance(self.base, RadiusAggregationCache) and tokens and _lnamd_hip.supported(layer, tokens):
+            side = math.isqrt(tokens[0].shape[1] - 1)
+            if side != 37 or len(tokens) != 1 or layer.r != 3:
+                raise ValueError('super_fast requires one layer, r=3 and a 37x37 source patch grid')
+            pooled = _lnamd_hip.lnamd(tokens, [3], layout='rbplc', pool_side=PATCH_GRID)[0]
+            return pooled.cpu() if return_cpu else pooled
         features = self.base(layer, tokens, return_cpu=False)
         b, p, layers, c = features.shape
         side = math.isqrt(p)

@@ -4,6 +4,7 @@
     python musc-gpu_amd/musc_hip/kernels_bench.py lnamd [--n 83 --layers 4 --iters 3]
     python musc-gpu_amd/musc_hip/kernels_bench.py attention [--dtype fp32|fp16 --blocks 24]
     python musc-gpu_amd/musc_hip/kernels_bench.py copy [--mib 1024 --iters 3]
+    python musc-gpu_amd/musc_hip/kernels_bench.py super_fast [--n 83 --iters 3] (config 3 from tokens)
     python musc-gpu_amd/musc_hip/kernels_bench.py e2e --n 160 --iters 1       (config 5)
     python musc-gpu_amd/musc_hip/kernels_bench.py mfma_peak                   (device calibration)
     python musc-gpu_amd/musc_hip/kernels_bench.py msm lnamd copy --iters 1   (several in one process)
@@ -95,6 +96,37 @@ def bench_lnamd(args):
         gbps = nbytes / (ms / 1e3) / 1e9
         res[name] = {'avg_ms': ms, 'gbps': gbps, 'frac_hbm_peak': gbps / HBM_GBPS}
     return res
+
+
+def bench_super_fast(args):
+    """Config 3 from layer tokens: LNAMD r=3 with the 37 -> 28 adaptive pooling in the same
+    pass, MSM on the 784-patch pool (normalised rows), epilogue to 518 x 518."""
+    from musc_hip import pipeline
+    dev = torch.device('cuda:0')
+    n = args.n
+    toks = [synthetic.plumbing_tokens(n, 1370, 1024, seed=42).to(dev)]
+    ts, lnamd_ms, pair_ms = [], [], []
+    for it in range(args.iters + 1):
+        timing = {}
+        e0, e1 = _events()
+        e0.record()
+        pipeline.score_pool(toks, r_list=[3], image_size=518, pool_grid=28, timing=timing)
+        e1.record()
+        torch.cuda.synchronize()
+        if it > 0:
+            ts.append(e0.elapsed_time(e1))
+            lnamd_ms += [a.elapsed_time(b) for a, b in timing['lnamd']]
+            pair_ms += [a.elapsed_time(b) for a, b in timing['pairs']]
+        print(f'[super_fast] iteration {it} done', file=sys.stderr, flush=True)
+    total = sum(ts) / len(ts)
+    pair = sum(pair_ms) / len(pair_ms)
+    lnamd = sum(lnamd_ms) / len(lnamd_ms)
+    p = 784
+    flop = 1024.0 * p * p * n * (n - 1)
+    nbytes = 4.0 * n * (1370 * 1024 + p * 1024)     # tokens read once, pooled pool written once
+    return {'kernel': 'super_fast', 'n': n, 'total_ms': total, 'images_per_s': n / (total / 1e3),
+            'lnamd_pooled_ms': lnamd, 'lnamd_pooled_gbps': nbytes / (lnamd / 1e3) / 1e9, 'pair_ms': pair,
+            'pair_tflops': flop / (pair / 1e3) / 1e12}
 
 
 def bench_attention(args):
@@ -196,7 +228,8 @@ def bench_copy(args):
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument('kernels', nargs='+', choices=['msm', 'lnamd', 'attention', 'copy', 'e2e', 'mfma_peak'])
+    ap.add_argument('kernels', nargs='+', choices=['msm', 'lnamd', 'super_fast', 'attention', 'copy', 'e2e',
+                                                     'mfma_peak'])
     ap.add_argument('--n', type=int, default=83)
     ap.add_argument('--p', type=int, default=1369)
     ap.add_argument('--c', type=int, default=1024)
@@ -206,8 +239,8 @@ def main():
     ap.add_argument('--mib', type=int, default=1024)
     ap.add_argument('--iters', type=int, default=3)
     args = ap.parse_args()
-    table = {'msm': bench_msm, 'lnamd': bench_lnamd, 'attention': bench_attention, 'copy': bench_copy,
-             'e2e': bench_e2e, 'mfma_peak': bench_mfma_peak}
+    table = {'msm': bench_msm, 'lnamd': bench_lnamd, 'super_fast': bench_super_fast, 'attention': bench_attention,
+             'copy': bench_copy, 'e2e': bench_e2e, 'mfma_peak': bench_mfma_peak}
     for name in args.kernels:
         print(json.dumps(table[name](args)), flush=True)
 

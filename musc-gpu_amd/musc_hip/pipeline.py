@@ -25,18 +25,21 @@ from __future__ import annotations
 
 import torch
 
-from . import _MSM_hip, _epilogue_hip, _lnamd_hip, _super_fast
+from . import _MSM_hip, _epilogue_hip, _lnamd_hip
 from ._RsCIN_hip import RsCIN
 from . import _runtime as rt
 
 
-def lnamd_pools(tokens: list[torch.Tensor], r_list: list[int]) -> torch.Tensor:
+def lnamd_pools(tokens: list[torch.Tensor], r_list: list[int], pool_grid: int | None = None) -> torch.Tensor:
     """(R, L, N, P, C) fp32 LNAMD window sums of (x - mean), to be scored with normalize_rows.
 
     Scored with row normalisation these give exactly the features of musc.py:227-243
-    (LayerNorm, box mean, L2 normalisation), up to fp32 rounding.
+    (LayerNorm, box mean, L2 normalisation), up to fp32 rounding.  `pool_grid`
+    pools every patch grid to pool_grid x pool_grid in the same LNAMD pass (the
+    super_fast aggregation, models/modules/_super_fast.py:17-27, ahead of the L2
+    normalisation at musc.py:238); P is then pool_grid**2.
     """
-    return _lnamd_hip.lnamd(tokens, r_list, raw_sums=True, layout='rlbpc')
+    return _lnamd_hip.lnamd(tokens, r_list, raw_sums=True, layout='rlbpc', pool_side=pool_grid)
 
 
 def msm_all(pools: torch.Tensor, topmin_min: float = 0, topmin_max: float = 0.3,
@@ -91,11 +94,7 @@ def score_pool(tokens: list[torch.Tensor], r_list=(1, 3, 5), image_size: int = 5
     if timing is not None:
         lnamd_ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
         lnamd_ev[0].record()
-    pools = lnamd_pools(tokens, list(r_list))
-    if pool_grid is not None:
-        r, l, n, p, c = pools.shape
-        pooled = _super_fast.adaptive_pool(pools.view(r * l * n, p, c), pool_grid)
-        pools = pooled.view(r, l, n, pool_grid * pool_grid, c)
+    pools = lnamd_pools(tokens, list(r_list), pool_grid)
     if timing is not None:
         lnamd_ev[1].record()
         timing.setdefault('lnamd', []).append(lnamd_ev)
