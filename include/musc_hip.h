@@ -251,7 +251,7 @@ int musc_attention_weights_strided(const void* q, const void* k, int dtype, int 
  * sum_out = x + residual rounded to the dtype (the residual add of
  * transformer.py:247) and normalises that (ln_2 of :248).  sum_out may alias x or
  * residual.  width % (16 bytes / element size) == 0, width <= 2048 (fp16) / 1024
- * (fp32); 16-byte aligned buffers. */
+ * (fp32); 16-byte aligned buffers (weight and bias included). */
 int musc_layernorm_rows(const void* x, const void* residual, void* sum_out,
                         const float* weight, const float* bias, int dtype, int rows, int width,
                         float eps, void* y, hipStream_t stream);
@@ -268,6 +268,18 @@ int musc_activation(const void* x, void* y, int dtype, int mode, long long n, hi
  * floats).  *flop (host, may be NULL) receives the FLOP count of the launch, so
  * flop / time is the sustained fp32 MFMA rate of the device. */
 int musc_calibrate_mfma_f32(float* out, int blocks, int iters, double* flop, hipStream_t stream);
+
+/* HBM calibration (no counterpart in the reference; measurement aids).
+ * musc_calibrate_hbm_stream: mode 0 reads `bytes` of src (nontemporal loads), 1 writes
+ * `bytes` of dst, 2 copies src -> dst; one 16-byte vector per thread in a one-shot
+ * grid, the most HBM-friendly pattern (the achievable rate of the part).
+ * musc_calibrate_lnamd_pattern: the global access pattern of the LNAMD streaming
+ * kernel (tokens (layers, n, tokens_per_image, c) fp32 read once, n_radii writes of
+ * (n_radii, layers, n, P, c) fp32) with no arithmetic: the rate the pattern allows.
+ * c a multiple of 64; 16-byte aligned buffers. */
+int musc_calibrate_hbm_stream(int mode, const void* src, void* dst, long long bytes, hipStream_t stream);
+int musc_calibrate_lnamd_pattern(const float* tokens, float* out, int n, int layers, int tokens_per_image,
+                                 int c, int n_radii, hipStream_t stream);
 
 #ifdef __cplusplus
 }

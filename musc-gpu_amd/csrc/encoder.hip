@@ -83,11 +83,13 @@ __device__ inline float round_to(float v) {
 }
 
 // grid ceil(rows / kRowsPerBlock), block 256.  A row is width / N vectors; lane
-// handles vectors lane + 64 c for c < chunks (the last chunk may be partial).
-template <int kDtype, bool kAdd>
+// handles vectors lane + 64 c for c < kC (the last chunk may be partial).  All
+// loads of a row (x, residual, weight, bias) are issued before the first use, from
+// clamped indices, so a wave waits for memory once.
+template <int kDtype, bool kAdd, int kC>
 __global__ __launch_bounds__(kRowsPerBlock * kWave) void layernorm_rows_kernel(
     const void* x, const void* r, void* sum_out,  // sum_out may alias x or r (same element read, then written)
-    const float* __restrict__ w, const float* __restrict__ b, int rows, int width, int chunks, float eps,
+    const float* __restrict__ w, const float* __restrict__ b, int rows, int width, float eps,
     void* __restrict__ y) {
   // no contraction: every fp32 result is formed, then rounded to fp16 (a fused
   // multiply-and-convert would round once and differ from torch at ties)
@@ -98,50 +100,58 @@ __global__ __launch_bounds__(kRowsPerBlock * kWave) void layernorm_rows_kernel(
   if (row >= rows) return;
   const int vrow = width / N;
   const long long row_vec = (long long)row * vrow;
-  float v[kMaxChunks][N];
+  float v[kC][N], rv[kC][N], wv[kC][N], bv[kC][N];
+  bool ok[kC];
+#pragma unroll
+  for (int c = 0; c < kC; ++c) {
+    const int col = c * kWave + lane;
+    ok[c] = col < vrow;
+    const int cc = ok[c] ? col : vrow - 1;
+    load_vec<kDtype>(x, row_vec + cc, v[c]);
+    if constexpr (kAdd) load_vec<kDtype>(r, row_vec + cc, rv[c]);
+    if (w) {
+      load_vec<MUSC_DTYPE_F32>(w + (long long)cc * N, 0, *reinterpret_cast<float(*)[4]>(&wv[c][0]));
+      if constexpr (N == 8) load_vec<MUSC_DTYPE_F32>(w + (long long)cc * N + 4, 0, *reinterpret_cast<float(*)[4]>(&wv[c][4]));
+    } else {
+#pragma unroll
+      for (int j = 0; j < N; ++j) wv[c][j] = 1.f;
+    }
+    if (b) {
+      load_vec<MUSC_DTYPE_F32>(b + (long long)cc * N, 0, *reinterpret_cast<float(*)[4]>(&bv[c][0]));
+      if constexpr (N == 8) load_vec<MUSC_DTYPE_F32>(b + (long long)cc * N + 4, 0, *reinterpret_cast<float(*)[4]>(&bv[c][4]));
+    } else {
+#pragma unroll
+      for (int j = 0; j < N; ++j) bv[c][j] = 0.f;
+    }
+  }
   float s = 0.f;
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c) {
+  for (int c = 0; c < kC; ++c) {
+    if constexpr (kAdd) {
 #pragma unroll
-    for (int j = 0; j < N; ++j) v[c][j] = 0.f;
-    if (c < chunks && c * kWave + lane < vrow) {
-      const long long idx = row_vec + c * kWave + lane;
-      load_vec<kDtype>(x, idx, v[c]);
-      if constexpr (kAdd) {
-        float rv[N];
-        load_vec<kDtype>(r, idx, rv);
-#pragma unroll
-        for (int j = 0; j < N; ++j) v[c][j] = round_to<kDtype>(v[c][j] + rv[j]);
-        store_vec<kDtype>(sum_out, idx, v[c]);
-      }
-#pragma unroll
-      for (int j = 0; j < N; ++j) s += v[c][j];
+      for (int j = 0; j < N; ++j) v[c][j] = round_to<kDtype>(v[c][j] + rv[c][j]);
+      if (ok[c]) store_vec<kDtype>(sum_out, row_vec + c * kWave + lane, v[c]);
     }
+#pragma unroll
+    for (int j = 0; j < N; ++j) s += ok[c] ? v[c][j] : 0.f;
   }
   const float mean = wave_sum(s) / (float)width;
   float q = 0.f;
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c)
-    if (c < chunks && c * kWave + lane < vrow) {
+  for (int c = 0; c < kC; ++c)
 #pragma unroll
-      for (int j = 0; j < N; ++j) {
-        const float d = v[c][j] - mean;
-        q += d * d;
-      }
+    for (int j = 0; j < N; ++j) {
+      const float d = v[c][j] - mean;
+      q += ok[c] ? d * d : 0.f;
     }
   const float rstd = 1.f / sqrtf(wave_sum(q) / (float)width + eps);
 #pragma unroll
-  for (int c = 0; c < kMaxChunks; ++c)
-    if (c < chunks && c * kWave + lane < vrow) {
-      const int col0 = (c * kWave + lane) * N;
-      float o[N];
+  for (int c = 0; c < kC; ++c) {
+    float o[N];
 #pragma unroll
-      for (int j = 0; j < N; ++j) {
-        const float wj = w ? w[col0 + j] : 1.f, bj = b ? b[col0 + j] : 0.f;
-        o[j] = as_fp32((v[c][j] - mean) * rstd * wj + bj);
-      }
-      store_vec<kDtype>(y, row_vec + c * kWave + lane, o);
-    }
+    for (int j = 0; j < N; ++j) o[j] = as_fp32((v[c][j] - mean) * rstd * wv[c][j] + bv[c][j]);
+    if (ok[c]) store_vec<kDtype>(y, row_vec + c * kWave + lane, o);
+  }
 }
 
 // n / N vectors, grid-stride.  mode 0: QuickGELU, mode 1: GELU (erf).
@@ -184,26 +194,29 @@ extern "C" int musc_layernorm_rows(const void* x, const void* residual, void* su
   const int n = dtype == MUSC_DTYPE_F32 ? 4 : 8;
   if (width % n != 0 || (width / n + kWave - 1) / kWave > enc::kMaxChunks) return MUSC_ERR_UNSUPPORTED;
   const uintptr_t addr = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
-                         reinterpret_cast<uintptr_t>(residual) | reinterpret_cast<uintptr_t>(sum_out);
+                         reinterpret_cast<uintptr_t>(residual) | reinterpret_cast<uintptr_t>(sum_out) |
+                         reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(bias);
   if (addr % 16) return MUSC_ERR_INVALID_ARG;
   if (rows == 0) return MUSC_OK;
   const int chunks = (width / n + kWave - 1) / kWave;
   const dim3 grid((unsigned)((rows + enc::kRowsPerBlock - 1) / enc::kRowsPerBlock)), block(enc::kRowsPerBlock * kWave);
-  if (dtype == MUSC_DTYPE_F32) {
-    if (residual)
-      hipLaunchKernelGGL((enc::layernorm_rows_kernel<MUSC_DTYPE_F32, true>), grid, block, 0, stream, x, residual,
-                         sum_out, weight, bias, rows, width, chunks, eps, y);
-    else
-      hipLaunchKernelGGL((enc::layernorm_rows_kernel<MUSC_DTYPE_F32, false>), grid, block, 0, stream, x, nullptr,
-                         nullptr, weight, bias, rows, width, chunks, eps, y);
-  } else {
-    if (residual)
-      hipLaunchKernelGGL((enc::layernorm_rows_kernel<MUSC_DTYPE_F16, true>), grid, block, 0, stream, x, residual,
-                         sum_out, weight, bias, rows, width, chunks, eps, y);
-    else
-      hipLaunchKernelGGL((enc::layernorm_rows_kernel<MUSC_DTYPE_F16, false>), grid, block, 0, stream, x, nullptr,
-                         nullptr, weight, bias, rows, width, chunks, eps, y);
+#define MUSC_LN_LAUNCH(DT, ADD, C)                                                                               \
+  hipLaunchKernelGGL((enc::layernorm_rows_kernel<DT, ADD, C>), grid, block, 0, stream, x, residual, sum_out, weight, \
+                     bias, rows, width, eps, y)
+#define MUSC_LN_CHUNKS(DT, ADD)                                                                                  \
+  switch (chunks) {                                                                                              \
+    case 1: MUSC_LN_LAUNCH(DT, ADD, 1); break;                                                                   \
+    case 2: MUSC_LN_LAUNCH(DT, ADD, 2); break;                                                                   \
+    case 3: MUSC_LN_LAUNCH(DT, ADD, 3); break;                                                                   \
+    default: MUSC_LN_LAUNCH(DT, ADD, 4); break;                                                                  \
   }
+  if (dtype == MUSC_DTYPE_F32) {
+    if (residual) { MUSC_LN_CHUNKS(MUSC_DTYPE_F32, true) } else { MUSC_LN_CHUNKS(MUSC_DTYPE_F32, false) }
+  } else {
+    if (residual) { MUSC_LN_CHUNKS(MUSC_DTYPE_F16, true) } else { MUSC_LN_CHUNKS(MUSC_DTYPE_F16, false) }
+  }
+#undef MUSC_LN_CHUNKS
+#undef MUSC_LN_LAUNCH
   return check_launch();
 }
 

@@ -7,6 +7,7 @@
     python musc-gpu_amd/musc_hip/kernels_bench.py super_fast [--n 83 --iters 3] (config 3 from tokens)
     python musc-gpu_amd/musc_hip/kernels_bench.py e2e --n 160 --iters 1       (config 5)
     python musc-gpu_amd/musc_hip/kernels_bench.py mfma_peak                   (device calibration)
+    python musc-gpu_amd/musc_hip/kernels_bench.py hbm                         (HBM calibration)
     python musc-gpu_amd/musc_hip/kernels_bench.py msm lnamd copy --iters 1   (several in one process)
 
 Each prints one JSON line with the average duration of the kernel(s) from HIP
@@ -129,6 +130,52 @@ def bench_super_fast(args):
             'pair_tflops': flop / (pair / 1e3) / 1e12}
 
 
+def bench_hbm(args):
+    """Achievable HBM rates (one-shot read / write / copy of 2 GiB) and the rate of the LNAMD
+    stream kernel's access pattern replayed without arithmetic at config 2's shape."""
+    import ctypes
+    dev = torch.device('cuda:0')
+    lib, s = rt.library(), rt.stream(dev)
+    res = {'kernel': 'hbm'}
+    nbytes = 2 << 30
+    src = torch.zeros(nbytes // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for mode, name, moved in ((0, 'read', nbytes), (1, 'write', nbytes), (2, 'copy', 2 * nbytes)):
+        ts = []
+        for it in range(args.iters + 1):
+            e0, e1 = _events()
+            e0.record()
+            rt.check(lib.musc_calibrate_hbm_stream(mode, src.data_ptr(), dst.data_ptr(), nbytes, s),
+                     'musc_calibrate_hbm_stream')
+            e1.record()
+            torch.cuda.synchronize()
+            if it > 0:
+                ts.append(e0.elapsed_time(e1))
+        ms = sum(ts) / len(ts)
+        res[name] = {'bytes': moved, 'avg_ms': ms, 'gbps': moved / (ms / 1e3) / 1e9,
+                     'frac_hbm_peak': moved / (ms / 1e3) / 1e9 / HBM_GBPS}
+        print(f'[hbm] {name} done', file=sys.stderr, flush=True)
+    del src, dst
+    n, L, T, C, R = 83, 4, 1370, 1024, 3
+    toks = torch.zeros((L, n, T, C), dtype=torch.float32, device=dev)
+    out = torch.empty((R, L, n, T - 1, C), dtype=torch.float32, device=dev)
+    moved = 4.0 * n * L * ((T - 1) * C + R * (T - 1) * C)
+    ts = []
+    for it in range(args.iters + 1):
+        e0, e1 = _events()
+        e0.record()
+        rt.check(lib.musc_calibrate_lnamd_pattern(toks.data_ptr(), out.data_ptr(), n, L, T, C, R, s),
+                 'musc_calibrate_lnamd_pattern')
+        e1.record()
+        torch.cuda.synchronize()
+        if it > 0:
+            ts.append(e0.elapsed_time(e1))
+    ms = sum(ts) / len(ts)
+    res['lnamd_pattern'] = {'bytes': moved, 'avg_ms': ms, 'gbps': moved / (ms / 1e3) / 1e9,
+                            'frac_hbm_peak': moved / (ms / 1e3) / 1e9 / HBM_GBPS}
+    return res
+
+
 def bench_attention(args):
     dev = torch.device('cuda:0')
     dtype = torch.float32 if args.dtype == 'fp32' else torch.float16
@@ -229,7 +276,7 @@ def bench_copy(args):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('kernels', nargs='+', choices=['msm', 'lnamd', 'super_fast', 'attention', 'copy', 'e2e',
-                                                     'mfma_peak'])
+                                                     'mfma_peak', 'hbm'])
     ap.add_argument('--n', type=int, default=83)
     ap.add_argument('--p', type=int, default=1369)
     ap.add_argument('--c', type=int, default=1024)
@@ -240,7 +287,7 @@ def main():
     ap.add_argument('--iters', type=int, default=3)
     args = ap.parse_args()
     table = {'msm': bench_msm, 'lnamd': bench_lnamd, 'super_fast': bench_super_fast, 'attention': bench_attention,
-             'copy': bench_copy, 'e2e': bench_e2e, 'mfma_peak': bench_mfma_peak}
+             'copy': bench_copy, 'e2e': bench_e2e, 'mfma_peak': bench_mfma_peak, 'hbm': bench_hbm}
     for name in args.kernels:
         print(json.dumps(table[name](args)), flush=True)
 
