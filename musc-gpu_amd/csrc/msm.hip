@@ -159,11 +159,14 @@ __device__ inline void store_chunk(float* __restrict__ dst, const float4 (&reg)[
     *reinterpret_cast<float4*>(dst + (lrow + 32 * i) * PITCH + lk) = reg[i];
 }
 
-template <bool kVec4>
+// kSplit (p >= BM): a 128-row or 128-column range holds at most one image boundary,
+// so tiles straddling a boundary reduce in registers too, with two image segments
+// per dimension; otherwise (small p) they go through the LDS epilogue.
+template <bool kVec4, bool kSplit>
 __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
     const float* __restrict__ z, const float* __restrict__ norms, const float* __restrict__ inv,
     uint32_t* __restrict__ minbits, int rows, int n, int p, int c, int T, long long ntiles) {
-  __shared__ __attribute__((aligned(16))) float smem[kSmemFloats];
+  __shared__ __attribute__((aligned(16))) float smem[kSplit ? kStageFloats : kSmemFloats];
   __shared__ __attribute__((aligned(16))) float s_rnorm[BM];
   __shared__ __attribute__((aligned(16))) float s_cnorm[BN];
   __shared__ __attribute__((aligned(16))) float s_rinv[BM];   // row scales (1 unless normalising)
@@ -347,6 +350,139 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
     return;
   }
 
+  if constexpr (kSplit) {
+    // Two-segment register epilogue.  Rows of this tile belong to image rA (local
+    // index below the boundary) or rA + 1, columns to cA or cA + 1; padding rows
+    // and columns carry image n.  Same-image and padding pairs are masked to +inf,
+    // then row and column minima are taken per segment of the other dimension.
+    const float inf = __int_as_float(kInfBits);
+    const int rA = rimg0, cA = cimg0;
+    float d2[2][2][16];
+    bool rowB[2][16];  // row lies in segment B (image rA + 1)
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int i0 = wm * 64 + mb * 32 + g * 8 + lh * 4;
+        const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[i0]);
+        const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[i0]);
+        const int4 rim = *reinterpret_cast<const int4*>(&s_rimg[i0]);
+        const float rv[4] = {rn.x, rn.y, rn.z, rn.w};
+        const float rs[4] = {-2.f * ri.x, -2.f * ri.y, -2.f * ri.z, -2.f * ri.w};
+        const int rimg[4] = {rim.x, rim.y, rim.z, rim.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rowB[mb][g * 4 + e] = rimg[e] != rA;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          const int j = wn * 64 + nb * 32 + lr;
+          const float cn = s_cnorm[j];
+          const float ci = s_cinv[j];
+          const int cimg = s_cimg[j];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float v = fmaxf(fmaf(rs[e] * ci, acc[mb][nb][g * 4 + e], rv[e] + cn), 0.f);
+            const bool masked = rimg[e] == cimg || rimg[e] == n || cimg == n;
+            d2[mb][nb][g * 4 + e] = masked ? inf : v;
+          }
+        }
+      }
+    // column minima over this wave's 64 rows, per row segment, then across lane halves
+    float cminA[2], cminB[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      float a = inf, b = inf;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float x = d2[mb][nb][v];
+          a = rowB[mb][v] ? a : fminf(a, x);
+          b = rowB[mb][v] ? fminf(b, x) : b;
+        }
+      cminA[nb] = a;
+      cminB[nb] = b;
+    }
+    {
+      const float sendA = lh ? cminA[0] : cminA[1], keepA = lh ? cminA[1] : cminA[0];
+      const float sendB = lh ? cminB[0] : cminB[1], keepB = lh ? cminB[1] : cminB[0];
+      cminA[0] = fminf(keepA, __shfl_xor(sendA, 32, kWave));
+      cminB[0] = fminf(keepB, __shfl_xor(sendB, 32, kWave));
+    }
+    // row minima over this wave's 64 columns, per column segment: transposing
+    // butterflies as in the single-segment path, one per segment
+    const bool colB0 = s_cimg[wn * 64 + lr] != cA, colB1 = s_cimg[wn * 64 + 32 + lr] != cA;
+    float rowminA, rowminB;
+    {
+      float rv[32];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          rv[mb * 16 + v] = fminf(colB0 ? inf : d2[mb][0][v], colB1 ? inf : d2[mb][1][v]);
+#pragma unroll
+      for (int bit = 4; bit >= 0; --bit) {
+        const int half = 1 << bit;
+        const bool up = (lr >> bit) & 1;
+#pragma unroll
+        for (int q = 0; q < half; ++q) {
+          const float send = up ? rv[q] : rv[q + half];
+          const float keep = up ? rv[q + half] : rv[q];
+          rv[q] = fminf(keep, __shfl_xor(send, half, kWave));
+        }
+      }
+      rowminA = rv[0];
+    }
+    {
+      float rv[32];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          rv[mb * 16 + v] = fminf(colB0 ? d2[mb][0][v] : inf, colB1 ? d2[mb][1][v] : inf);
+#pragma unroll
+      for (int bit = 4; bit >= 0; --bit) {
+        const int half = 1 << bit;
+        const bool up = (lr >> bit) & 1;
+#pragma unroll
+        for (int q = 0; q < half; ++q) {
+          const float send = up ? rv[q] : rv[q + half];
+          const float keep = up ? rv[q + half] : rv[q];
+          rv[q] = fminf(keep, __shfl_xor(send, half, kWave));
+        }
+      }
+      rowminB = rv[0];
+    }
+    __syncthreads();  // operand buffers are no longer read
+    float* s_cminA = smem;            // [2 (wm)][BN]
+    float* s_cminB = smem + 2 * BN;
+    float* s_rminA = smem + 4 * BN;   // [2 (wn)][BM]
+    float* s_rminB = smem + 4 * BN + 2 * BM;
+    s_cminA[wm * BN + wn * 64 + lh * 32 + lr] = cminA[0];
+    s_cminB[wm * BN + wn * 64 + lh * 32 + lr] = cminB[0];
+    const int rk = wm * 64 + (lr >> 4) * 32 + ((lr & 15) >> 2) * 8 + lh * 4 + (lr & 3);
+    s_rminA[wn * BM + rk] = rowminA;
+    s_rminB[wn * BM + rk] = rowminB;
+    __syncthreads();
+    if (t < BM) {
+      const int r = row0 + t;
+      if (r < rows) {
+        const float a = fminf(s_rminA[t], s_rminA[BM + t]);
+        const float b = fminf(s_rminB[t], s_rminB[BM + t]);
+        if (a < inf) atomicMin(minbits + (long long)r * n + cA, __float_as_uint(a));
+        if (b < inf) atomicMin(minbits + (long long)r * n + cA + 1, __float_as_uint(b));
+      }
+    } else {
+      const int j = t - BM;
+      const int cc = col0 + j;
+      if (cc < rows) {
+        const float a = fminf(s_cminA[j], s_cminA[BN + j]);
+        const float b = fminf(s_cminB[j], s_cminB[BN + j]);
+        if (a < inf) atomicMin(minbits + (long long)cc * n + rA, __float_as_uint(a));
+        if (b < inf) atomicMin(minbits + (long long)cc * n + rA + 1, __float_as_uint(b));
+      }
+    }
+    return;
+  } else {
   // Epilogue: squared distances into LDS (the operand buffers are free now).
   float* E = smem;
 #pragma unroll
@@ -405,6 +541,7 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
       }
       if (seg < n && cur < __int_as_float(kInfBits)) atomicMin(dst + seg, __float_as_uint(cur));
     }
+  }
   }
 }
 
@@ -502,12 +639,16 @@ inline int run_pairs(const float* z, int n, int p, int c, const Workspace& w, hi
   const long long ntiles = total_tiles(T);
   const long long grid = (ntiles + kXcds - 1) / kXcds * kXcds;
   if (grid > 0x7fffffffLL) return MUSC_ERR_UNSUPPORTED;
-  if ((c & 3) == 0)
-    hipLaunchKernelGGL(msm_pair_min_kernel<true>, dim3((unsigned)grid), dim3(THREADS), 0, s, z, w.norms,
-                       w.inv, w.minbits, (int)rows, n, p, c, (int)T, ntiles);
-  else
-    hipLaunchKernelGGL(msm_pair_min_kernel<false>, dim3((unsigned)grid), dim3(THREADS), 0, s, z, w.norms,
-                       w.inv, w.minbits, (int)rows, n, p, c, (int)T, ntiles);
+#define MUSC_PAIR_LAUNCH(V4, SPLIT)                                                                              \
+  hipLaunchKernelGGL((msm_pair_min_kernel<V4, SPLIT>), dim3((unsigned)grid), dim3(THREADS), 0, s, z, w.norms, w.inv, \
+                     w.minbits, (int)rows, n, p, c, (int)T, ntiles)
+  const bool split = p >= BM;
+  if ((c & 3) == 0) {
+    if (split) MUSC_PAIR_LAUNCH(true, true); else MUSC_PAIR_LAUNCH(true, false);
+  } else {
+    if (split) MUSC_PAIR_LAUNCH(false, true); else MUSC_PAIR_LAUNCH(false, false);
+  }
+#undef MUSC_PAIR_LAUNCH
   return check_launch();
 }
 

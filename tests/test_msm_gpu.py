@@ -26,8 +26,11 @@ def test_golden(golden, device, case):
     np.testing.assert_allclose(near, g[f'{case}_nearest'], rtol=0, atol=ATOL)
 
 
+# p >= 128 takes the two-segment register epilogue for tiles straddling an image boundary
+# (p = 128: every tile inside one image; 129/130/200/257/300/1369: straddling tiles, padded
+# last tile row); p < 128 the LDS epilogue (several images per tile); c % 4 != 0 the masked loads
 @pytest.mark.parametrize('n,p,c', [(5, 200, 36), (9, 130, 1024), (17, 64, 100), (6, 129, 7), (12, 257, 33),
-                                   (40, 3, 4)])
+                                   (40, 3, 4), (7, 128, 64), (5, 300, 1024), (5, 1369, 64)])
 def test_random_shapes_vs_oracles(device, n, p, c):
     torch.manual_seed(n * 1000 + p)
     z = torch.nn.functional.normalize(torch.randn((n, p, c)), dim=-1)
