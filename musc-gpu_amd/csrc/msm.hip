@@ -21,6 +21,8 @@
 //                            The distance matrix never reaches HBM.
 //   4. msm_rank_kernel       one wave per patch: rank the n-1 minima, average the
 //                            square roots of ranks [a, b).
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace musc {
@@ -157,6 +159,44 @@ __device__ inline void store_chunk(float* __restrict__ dst, const float4 (&reg)[
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     *reinterpret_cast<float4*>(dst + (lrow + 32 * i) * PITCH + lk) = reg[i];
+}
+
+// Partner value for stage `half` of the transposing min-butterfly over the 32 lanes
+// of a half-wave.  Stages 8, 4, 2, 1 use DPP within 16-lane rows (row_ror:8 = lane
+// ^ 8; row_half_mirror = lane ^ 7, which flips bit 2 like lane ^ 4 and is an
+// equally valid pairing: a lane keeps the half of its items selected by the bit
+// being resolved, its partner holds the complementary half of the same item set,
+// and the partners met over the five stages still span all 32 lanes); stage 16
+// goes through ds_bpermute.
+template <int kHalf>
+__device__ inline float butterfly_partner(float v) {
+  const int x = __builtin_bit_cast(int, v);
+  if constexpr (kHalf == 1) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0xb1, 0xf, 0xf, false));
+  if constexpr (kHalf == 2) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x4e, 0xf, 0xf, false));
+  if constexpr (kHalf == 4) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x141, 0xf, 0xf, false));
+  if constexpr (kHalf == 8) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x128, 0xf, 0xf, false));
+  return __shfl_xor(v, kHalf, kWave);
+}
+
+// rv[0] of lane lr ends with min over the 32 lanes of item k = lr (items = 32
+// values per lane).
+__device__ inline float transpose_min32(float (&rv)[32], int lr) {
+  auto stage = [&](auto half_c) {
+    constexpr int half = decltype(half_c)::value;
+    const bool up = (lr & half) != 0;
+#pragma unroll
+    for (int q = 0; q < half; ++q) {
+      const float send = up ? rv[q] : rv[q + half];
+      const float keep = up ? rv[q + half] : rv[q];
+      rv[q] = fminf(keep, butterfly_partner<half>(send));
+    }
+  };
+  stage(std::integral_constant<int, 16>{});
+  stage(std::integral_constant<int, 8>{});
+  stage(std::integral_constant<int, 4>{});
+  stage(std::integral_constant<int, 2>{});
+  stage(std::integral_constant<int, 1>{});
+  return rv[0];
 }
 
 // kSplit (p >= BM): a 128-row or 128-column range holds at most one image boundary,
@@ -322,17 +362,7 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) rv[mb * 16 + v] = fminf(d2[mb][0][v], d2[mb][1][v]);
-#pragma unroll
-    for (int bit = 4; bit >= 0; --bit) {
-      const int half = 1 << bit;
-      const bool up = (lr >> bit) & 1;
-#pragma unroll
-      for (int q = 0; q < half; ++q) {
-        const float send = up ? rv[q] : rv[q + half];
-        const float keep = up ? rv[q + half] : rv[q];
-        rv[q] = fminf(keep, __shfl_xor(send, half, kWave));
-      }
-    }
+    transpose_min32(rv, lr);
     __syncthreads();  // operand buffers are no longer read
     float* s_cmin = smem;             // [2 (wm)][BN]
     float* s_rmin = smem + 2 * BN;    // [2 (wn)][BM]
@@ -419,17 +449,7 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
 #pragma unroll
         for (int v = 0; v < 16; ++v)
           rv[mb * 16 + v] = fminf(colB0 ? inf : d2[mb][0][v], colB1 ? inf : d2[mb][1][v]);
-#pragma unroll
-      for (int bit = 4; bit >= 0; --bit) {
-        const int half = 1 << bit;
-        const bool up = (lr >> bit) & 1;
-#pragma unroll
-        for (int q = 0; q < half; ++q) {
-          const float send = up ? rv[q] : rv[q + half];
-          const float keep = up ? rv[q + half] : rv[q];
-          rv[q] = fminf(keep, __shfl_xor(send, half, kWave));
-        }
-      }
+      transpose_min32(rv, lr);
       rowminA = rv[0];
     }
     {
@@ -439,17 +459,7 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
 #pragma unroll
         for (int v = 0; v < 16; ++v)
           rv[mb * 16 + v] = fminf(colB0 ? d2[mb][0][v] : inf, colB1 ? d2[mb][1][v] : inf);
-#pragma unroll
-      for (int bit = 4; bit >= 0; --bit) {
-        const int half = 1 << bit;
-        const bool up = (lr >> bit) & 1;
-#pragma unroll
-        for (int q = 0; q < half; ++q) {
-          const float send = up ? rv[q] : rv[q + half];
-          const float keep = up ? rv[q + half] : rv[q];
-          rv[q] = fminf(keep, __shfl_xor(send, half, kWave));
-        }
-      }
+      transpose_min32(rv, lr);
       rowminB = rv[0];
     }
     __syncthreads();  // operand buffers are no longer read
