@@ -276,10 +276,11 @@ int musc_calibrate_mfma_f32(float* out, int blocks, int iters, double* flop, hip
  * musc_calibrate_lnamd_pattern: the global access pattern of the LNAMD streaming
  * kernel (tokens (layers, n, tokens_per_image, c) fp32 read once, n_radii writes of
  * (n_radii, layers, n, P, c) fp32) with no arithmetic: the rate the pattern allows.
+ * mode 0 replays reads and writes, 1 only the writes, 2 only the reads.
  * c a multiple of 64; 16-byte aligned buffers. */
 int musc_calibrate_hbm_stream(int mode, const void* src, void* dst, long long bytes, hipStream_t stream);
 int musc_calibrate_lnamd_pattern(const float* tokens, float* out, int n, int layers, int tokens_per_image,
-                                 int c, int n_radii, hipStream_t stream);
+                                 int c, int n_radii, int mode, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -57,7 +57,9 @@ extern "C" int musc_calibrate_mfma_f32(float* out, int blocks, int iters, double
 // (workgroup per (image, layer, 64-channel slice), thread (column, 4 channels)
 // sweeping the rows, one float4 read per input row and n_radii float4 writes per
 // output row into the (R, L, N, P, C) pools) with no arithmetic, LDS or barriers:
-// the rate that access pattern itself allows.
+// the rate that access pattern itself allows.  kMode 0 replays reads and writes,
+// 1 only the writes, 2 only the reads, so the cost of interleaving the two on HBM
+// is the difference between mode 0 and the sum of modes 1 and 2.
 // ---------------------------------------------------------------------------
 namespace musc {
 namespace cal {
@@ -82,6 +84,7 @@ __global__ __launch_bounds__(1024) void hbm_stream_kernel(const cal_f4* __restri
 
 constexpr int kPatCg = 16;
 
+template <int kMode>
 __global__ __launch_bounds__(1024) void lnamd_pattern_kernel(const cal_f4* __restrict__ tokens,
                                                              cal_f4* __restrict__ out, int n, int layers, int tpi,
                                                              int c, int side, int n_radii) {
@@ -94,12 +97,17 @@ __global__ __launch_bounds__(1024) void lnamd_pattern_kernel(const cal_f4* __res
   const long long in0 = ((long long)l * n * tpi + (long long)b * tpi + 1) * c4 + (long long)w * c4 + g;
   cal_f4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int h = 0; h < side; ++h) {
-    acc += __builtin_nontemporal_load(tokens + in0 + (long long)h * side * c4);
+    if constexpr (kMode != 1) acc += __builtin_nontemporal_load(tokens + in0 + (long long)h * side * c4);
     const long long p = (long long)h * side + w;
-    for (int k = 0; k < n_radii; ++k) {
-      const long long o = ((((long long)k * layers + l) * n + b) * P + p) * c4 + g;
-      __builtin_nontemporal_store(acc, out + o);
+    if constexpr (kMode != 2) {
+      for (int k = 0; k < n_radii; ++k) {
+        const long long o = ((((long long)k * layers + l) * n + b) * P + p) * c4 + g;
+        __builtin_nontemporal_store(acc, out + o);
+      }
     }
+  }
+  if constexpr (kMode == 2) {
+    if (acc.x == 1234.5f && acc.y == -1234.5f) out[0] = acc;  // keeps the loads; never true for the fill used
   }
 }
 
@@ -125,16 +133,26 @@ extern "C" int musc_calibrate_hbm_stream(int mode, const void* src, void* dst, l
 }
 
 extern "C" int musc_calibrate_lnamd_pattern(const float* tokens, float* out, int n, int layers, int tokens_per_image,
-                                            int c, int n_radii, hipStream_t stream) {
+                                            int c, int n_radii, int mode, hipStream_t stream) {
   if (!tokens || !out || n < 1 || layers < 1 || n_radii < 1 || c < 4 * cal::kPatCg) return MUSC_ERR_INVALID_ARG;
+  if (mode < 0 || mode > 2) return MUSC_ERR_INVALID_ARG;
   if (c % (4 * cal::kPatCg)) return MUSC_ERR_UNSUPPORTED;
   int side = 0;
   while ((side + 1) * (side + 1) <= tokens_per_image - 1) ++side;
   if (side * side != tokens_per_image - 1 || side * cal::kPatCg > 1024) return MUSC_ERR_INVALID_ARG;
   if ((reinterpret_cast<uintptr_t>(tokens) | reinterpret_cast<uintptr_t>(out)) % 16) return MUSC_ERR_INVALID_ARG;
   const long long grid = (long long)n * layers * (c / 4 / cal::kPatCg);
-  hipLaunchKernelGGL(cal::lnamd_pattern_kernel, dim3((unsigned)grid), dim3(side * cal::kPatCg), 0, stream,
-                     reinterpret_cast<const cal::cal_f4*>(tokens), reinterpret_cast<cal::cal_f4*>(out), n, layers,
-                     tokens_per_image, c, side, n_radii);
+  const auto* tk = reinterpret_cast<const cal::cal_f4*>(tokens);
+  auto* o = reinterpret_cast<cal::cal_f4*>(out);
+  const dim3 g((unsigned)grid), blk(side * cal::kPatCg);
+  if (mode == 0)
+    hipLaunchKernelGGL(cal::lnamd_pattern_kernel<0>, g, blk, 0, stream, tk, o, n, layers, tokens_per_image, c, side,
+                       n_radii);
+  else if (mode == 1)
+    hipLaunchKernelGGL(cal::lnamd_pattern_kernel<1>, g, blk, 0, stream, tk, o, n, layers, tokens_per_image, c, side,
+                       n_radii);
+  else
+    hipLaunchKernelGGL(cal::lnamd_pattern_kernel<2>, g, blk, 0, stream, tk, o, n, layers, tokens_per_image, c, side,
+                       n_radii);
   return check_launch();
 }

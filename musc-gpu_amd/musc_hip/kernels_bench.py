@@ -159,20 +159,24 @@ def bench_hbm(args):
     n, L, T, C, R = 83, 4, 1370, 1024, 3
     toks = torch.zeros((L, n, T, C), dtype=torch.float32, device=dev)
     out = torch.empty((R, L, n, T - 1, C), dtype=torch.float32, device=dev)
-    moved = 4.0 * n * L * ((T - 1) * C + R * (T - 1) * C)
-    ts = []
-    for it in range(args.iters + 1):
-        e0, e1 = _events()
-        e0.record()
-        rt.check(lib.musc_calibrate_lnamd_pattern(toks.data_ptr(), out.data_ptr(), n, L, T, C, R, s),
-                 'musc_calibrate_lnamd_pattern')
-        e1.record()
-        torch.cuda.synchronize()
-        if it > 0:
-            ts.append(e0.elapsed_time(e1))
-    ms = sum(ts) / len(ts)
-    res['lnamd_pattern'] = {'bytes': moved, 'avg_ms': ms, 'gbps': moved / (ms / 1e3) / 1e9,
-                            'frac_hbm_peak': moved / (ms / 1e3) / 1e9 / HBM_GBPS}
+    read_b, write_b = 4.0 * n * L * (T - 1) * C, 4.0 * n * L * R * (T - 1) * C
+    # mode 0: reads and writes interleaved as in the kernel; 1: writes only; 2: reads only
+    for mode, name, moved in ((0, 'lnamd_pattern', read_b + write_b), (1, 'lnamd_pattern_writes_only', write_b),
+                              (2, 'lnamd_pattern_reads_only', read_b)):
+        ts = []
+        for it in range(args.iters + 1):
+            e0, e1 = _events()
+            e0.record()
+            rt.check(lib.musc_calibrate_lnamd_pattern(toks.data_ptr(), out.data_ptr(), n, L, T, C, R, mode, s),
+                     'musc_calibrate_lnamd_pattern')
+            e1.record()
+            torch.cuda.synchronize()
+            if it > 0:
+                ts.append(e0.elapsed_time(e1))
+        ms = sum(ts) / len(ts)
+        res[name] = {'bytes': moved, 'avg_ms': ms, 'gbps': moved / (ms / 1e3) / 1e9,
+                     'frac_hbm_peak': moved / (ms / 1e3) / 1e9 / HBM_GBPS}
+        print(f'[hbm] {name} done', file=sys.stderr, flush=True)
     return res
 
 
