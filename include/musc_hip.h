@@ -104,6 +104,26 @@ int musc_msm_pair_minima_f32(const float* z, int n, int p, int c,
 int musc_msm_rank_f32(int n, int p, int rank_lo, int rank_hi, double* scores,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Split engine: the same scores, with each fp32 dot product formed from three
+ * fp16 MFMA products.  Rows are L2-normalised and scaled by 2^10, split as
+ * hi = fp16(v), lo = fp16(v - hi), and a.b is accumulated in fp32 as
+ * hi.hi + hi.lo + lo.hi (error below 2^-22 |a||b|, the order of fp32's own
+ * accumulation error); a per-row scale restores the units, so MUSC_MSM_NORMALIZE_ROWS
+ * and unnormalised inputs both work.  Same contract, arguments and stage order as
+ * the fp32 engine above (replaces the same reference interface,
+ * models/modules/_MSM_gpu.py:701-830), with a larger workspace (the split rows) and
+ * p >= 256 (MUSC_ERR_UNSUPPORTED otherwise).  musc_msm_rank_f32 accepts this
+ * workspace.  Choose the engine by shape and accuracy need: the fp32 engine is the
+ * reference-faithful default. */
+int musc_msm_split_workspace_bytes(int n, int p, int c, size_t* out);
+int musc_msm_split_prepare_f32(const float* z, int n, int p, int c, int flags,
+                               void* workspace, size_t workspace_bytes, hipStream_t stream);
+int musc_msm_split_pair_minima(int n, int p, int c, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream);
+int musc_msm_split_scores_f32(const float* z, int n, int p, int c, int rank_lo, int rank_hi,
+                              int flags, double* scores, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* LNAMD: per-image LayerNorm over (C,H,W) + r x r zero-padded box mean.     */
 /* ------------------------------------------------------------------------ */

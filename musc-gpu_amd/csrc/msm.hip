@@ -21,14 +21,10 @@
 //                            The distance matrix never reaches HBM.
 //   4. msm_rank_kernel       one wave per patch: rank the n-1 minima, average the
 //                            square roots of ranks [a, b).
-#include <type_traits>
-
-#include "common.hpp"
+#include "msm_common.hpp"
 
 namespace musc {
 namespace msm {
-
-typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128;          // tile rows (query patches)
 constexpr int BN = 128;          // tile columns (reference patches)
@@ -36,48 +32,10 @@ constexpr int BK = 32;           // K chunk (channels) per pipeline stage
 constexpr int PITCH = BK + 4;    // LDS row pitch in floats for staged operands
 constexpr int EPITCH = BN + 1;   // LDS row pitch of the epilogue distance tile
 constexpr int THREADS = 256;     // 4 waves, each owns a 64x64 sub-tile
-constexpr int BAND = 8;          // tile rows per band of the tile enumeration
-constexpr uint32_t kInfBits = 0x7f800000u;
 
 constexpr int kStageFloats = 2 * (BM + BN) * PITCH;       // double-buffered A and B
 constexpr int kEpiFloats = BM * EPITCH;
 constexpr int kSmemFloats = kStageFloats > kEpiFloats ? kStageFloats : kEpiFloats;
-
-// ---------------------------------------------------------------------------
-// Tile enumeration.  Tiles (I, J), I <= J < T, are numbered band by band (BAND
-// tile rows per band); inside a band the triangle (J < I0 + h) comes first,
-// then the rectangle in column-major order, so that the workgroups one XCD runs
-// at the same time share a few A and B panels.
-// ---------------------------------------------------------------------------
-__host__ __device__ inline long long band_prefix(long long s, long long T) {
-  // tiles in bands 0..s-1, all of which are full (BAND rows)
-  return 36LL * s + 8LL * (T - 8) * s - 32LL * s * (s - 1);
-}
-
-__host__ __device__ inline long long total_tiles(long long T) { return T * (T + 1) / 2; }
-
-__device__ inline int2 decode_tile(long long w, long long T) {
-  const long long nb = (T + BAND - 1) / BAND;
-  long long lo = 0, hi = nb - 1;  // largest s with band_prefix(s) <= w
-  while (lo < hi) {
-    long long mid = (lo + hi + 1) >> 1;
-    if (band_prefix(mid, T) <= w) lo = mid; else hi = mid - 1;
-  }
-  const long long s = lo;
-  const long long I0 = s * BAND;
-  const long long h = (T - I0) < BAND ? (T - I0) : BAND;
-  long long q = w - band_prefix(s, T);
-  const long long tri = h * (h + 1) / 2;
-  if (q < tri) {
-    long long jl = (long long)((sqrt(8.0 * (double)q + 1.0) - 1.0) * 0.5);
-    while ((jl + 1) * (jl + 2) / 2 <= q) ++jl;
-    while (jl * (jl + 1) / 2 > q) --jl;
-    const long long il = q - jl * (jl + 1) / 2;
-    return make_int2((int)(I0 + il), (int)(I0 + jl));
-  }
-  q -= tri;
-  return make_int2((int)(I0 + q % h), (int)(I0 + h + q / h));
-}
 
 // ---------------------------------------------------------------------------
 // Row norms.
@@ -90,18 +48,7 @@ __global__ __launch_bounds__(256) void msm_norms_kernel(const float* __restrict_
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const long long row = (long long)blockIdx.x * (blockDim.x / kWave) + wave;
   if (row >= rows) return;
-  const float* src = z + row * (long long)c;
-  double acc = 0.0;
-  if ((c & 3) == 0) {
-    const float4* s4 = reinterpret_cast<const float4*>(src);
-    for (int k = lane; k < c / 4; k += kWave) {
-      float4 v = s4[k];
-      acc += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
-    }
-  } else {
-    for (int k = lane; k < c; k += kWave) acc += (double)src[k] * src[k];
-  }
-  acc = wave_sum(acc);
+  const double acc = row_sumsq(z + row * (long long)c, c, lane);
   if (lane == 0) {
     if (normalize) {
       const double r = 1.0 / sqrt(acc);
@@ -159,44 +106,6 @@ __device__ inline void store_chunk(float* __restrict__ dst, const float4 (&reg)[
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     *reinterpret_cast<float4*>(dst + (lrow + 32 * i) * PITCH + lk) = reg[i];
-}
-
-// Partner value for stage `half` of the transposing min-butterfly over the 32 lanes
-// of a half-wave.  Stages 8, 4, 2, 1 use DPP within 16-lane rows (row_ror:8 = lane
-// ^ 8; row_half_mirror = lane ^ 7, which flips bit 2 like lane ^ 4 and is an
-// equally valid pairing: a lane keeps the half of its items selected by the bit
-// being resolved, its partner holds the complementary half of the same item set,
-// and the partners met over the five stages still span all 32 lanes); stage 16
-// goes through ds_bpermute.
-template <int kHalf>
-__device__ inline float butterfly_partner(float v) {
-  const int x = __builtin_bit_cast(int, v);
-  if constexpr (kHalf == 1) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0xb1, 0xf, 0xf, false));
-  if constexpr (kHalf == 2) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x4e, 0xf, 0xf, false));
-  if constexpr (kHalf == 4) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x141, 0xf, 0xf, false));
-  if constexpr (kHalf == 8) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x128, 0xf, 0xf, false));
-  return __shfl_xor(v, kHalf, kWave);
-}
-
-// rv[0] of lane lr ends with min over the 32 lanes of item k = lr (items = 32
-// values per lane).
-__device__ inline float transpose_min32(float (&rv)[32], int lr) {
-  auto stage = [&](auto half_c) {
-    constexpr int half = decltype(half_c)::value;
-    const bool up = (lr & half) != 0;
-#pragma unroll
-    for (int q = 0; q < half; ++q) {
-      const float send = up ? rv[q] : rv[q + half];
-      const float keep = up ? rv[q + half] : rv[q];
-      rv[q] = fminf(keep, butterfly_partner<half>(send));
-    }
-  };
-  stage(std::integral_constant<int, 16>{});
-  stage(std::integral_constant<int, 8>{});
-  stage(std::integral_constant<int, 4>{});
-  stage(std::integral_constant<int, 2>{});
-  stage(std::integral_constant<int, 1>{});
-  return rv[0];
 }
 
 // kSplit (p >= BM): a 128-row or 128-column range holds at most one image boundary,
@@ -603,27 +512,6 @@ __global__ __launch_bounds__(256) void msm_nearest_kernel(const uint32_t* __rest
   nearest[i] = (j == (int)(row / p)) ? __int_as_float(kInfBits) : sqrtf(__uint_as_float(minbits[i]));
 }
 
-struct Workspace {
-  float* norms;
-  float* inv;
-  uint32_t* minbits;
-};
-
-inline size_t workspace_bytes(long long n, long long p) {
-  const long long rows = n * p;
-  return 2 * align_up((size_t)rows * 4, 256) + align_up((size_t)rows * n * 4, 256);
-}
-
-inline Workspace carve(void* ws, long long n, long long p) {
-  const long long rows = n * p;
-  char* base = static_cast<char*>(ws);
-  Workspace w;
-  w.norms = reinterpret_cast<float*>(base);
-  w.inv = reinterpret_cast<float*>(base + align_up((size_t)rows * 4, 256));
-  w.minbits = reinterpret_cast<uint32_t*>(base + 2 * align_up((size_t)rows * 4, 256));
-  return w;
-}
-
 inline int validate(const float* z, int n, int p, int c, void* ws, size_t ws_bytes) {
   if (!z || n < 2 || p < 1 || c < 1) return MUSC_ERR_INVALID_ARG;
   const long long rows = (long long)n * p;
@@ -663,7 +551,7 @@ inline int run_pairs(const float* z, int n, int p, int c, const Workspace& w, hi
 }
 
 // Stage 3: trimmed rank means.
-inline int run_rank(int n, int p, int a, int b, double* scores, const Workspace& w, hipStream_t s) {
+int run_rank(int n, int p, int a, int b, double* scores, const Workspace& w, hipStream_t s) {
   const long long rows = (long long)n * p;
   const size_t smem = (size_t)kRankWaves * n * sizeof(float);
   hipLaunchKernelGGL(msm_rank_kernel, dim3((unsigned)((rows + kRankWaves - 1) / kRankWaves)),

@@ -1,0 +1,140 @@
+// Pieces shared by the two MSM pair-minima engines (msm.hip: fp32 MFMA;
+// msm_split.hip: fp32 products from three fp16 MFMA products): the
+// upper-triangular tile enumeration, the row squared norm, the transposing
+// min-butterfly of the register epilogues and the workspace layout.
+#pragma once
+
+#include <type_traits>
+
+#include "common.hpp"
+
+namespace musc {
+namespace msm {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int BAND = 8;  // tile rows per band of the tile enumeration
+constexpr uint32_t kInfBits = 0x7f800000u;
+
+// ---------------------------------------------------------------------------
+// Tile enumeration.  Tiles (I, J), I <= J < T, are numbered band by band (BAND
+// tile rows per band); inside a band the triangle (J < I0 + h) comes first,
+// then the rectangle in column-major order, so that the workgroups one XCD runs
+// at the same time share a few A and B panels.
+// ---------------------------------------------------------------------------
+__host__ __device__ inline long long band_prefix(long long s, long long T) {
+  // tiles in bands 0..s-1, all of which are full (BAND rows)
+  return 36LL * s + 8LL * (T - 8) * s - 32LL * s * (s - 1);
+}
+
+__host__ __device__ inline long long total_tiles(long long T) { return T * (T + 1) / 2; }
+
+__device__ inline int2 decode_tile(long long w, long long T) {
+  const long long nb = (T + BAND - 1) / BAND;
+  long long lo = 0, hi = nb - 1;  // largest s with band_prefix(s) <= w
+  while (lo < hi) {
+    long long mid = (lo + hi + 1) >> 1;
+    if (band_prefix(mid, T) <= w) lo = mid; else hi = mid - 1;
+  }
+  const long long s = lo;
+  const long long I0 = s * BAND;
+  const long long h = (T - I0) < BAND ? (T - I0) : BAND;
+  long long q = w - band_prefix(s, T);
+  const long long tri = h * (h + 1) / 2;
+  if (q < tri) {
+    long long jl = (long long)((sqrt(8.0 * (double)q + 1.0) - 1.0) * 0.5);
+    while ((jl + 1) * (jl + 2) / 2 <= q) ++jl;
+    while (jl * (jl + 1) / 2 > q) --jl;
+    const long long il = q - jl * (jl + 1) / 2;
+    return make_int2((int)(I0 + il), (int)(I0 + jl));
+  }
+  q -= tri;
+  return make_int2((int)(I0 + q % h), (int)(I0 + h + q / h));
+}
+
+// Sum of squares of one row in fp64, reduced over the wave (result in every lane).
+__device__ inline double row_sumsq(const float* __restrict__ src, int c, int lane) {
+  double acc = 0.0;
+  if ((c & 3) == 0) {
+    const float4* s4 = reinterpret_cast<const float4*>(src);
+    for (int k = lane; k < c / 4; k += kWave) {
+      float4 v = s4[k];
+      acc += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+    }
+  } else {
+    for (int k = lane; k < c; k += kWave) acc += (double)src[k] * src[k];
+  }
+  return wave_sum(acc);
+}
+
+// Partner value for stage `half` of the transposing min-butterfly over the 32 lanes
+// of a half-wave.  Stages 8, 4, 2, 1 use DPP within 16-lane rows (row_ror:8 = lane
+// ^ 8; row_half_mirror = lane ^ 7, which flips bit 2 like lane ^ 4 and is an
+// equally valid pairing: a lane keeps the half of its items selected by the bit
+// being resolved, its partner holds the complementary half of the same item set,
+// and the partners met over the five stages still span all 32 lanes); stage 16
+// goes through ds_bpermute.
+template <int kHalf>
+__device__ inline float butterfly_partner(float v) {
+  const int x = __builtin_bit_cast(int, v);
+  if constexpr (kHalf == 1) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0xb1, 0xf, 0xf, false));
+  if constexpr (kHalf == 2) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x4e, 0xf, 0xf, false));
+  if constexpr (kHalf == 4) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x141, 0xf, 0xf, false));
+  if constexpr (kHalf == 8) return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x128, 0xf, 0xf, false));
+  return __shfl_xor(v, kHalf, kWave);
+}
+
+// rv[0] of lane lr ends with min over the 32 lanes of item k = lr (items = 32
+// values per lane).
+__device__ inline float transpose_min32(float (&rv)[32], int lr) {
+  auto stage = [&](auto half_c) {
+    constexpr int half = decltype(half_c)::value;
+    const bool up = (lr & half) != 0;
+#pragma unroll
+    for (int q = 0; q < half; ++q) {
+      const float send = up ? rv[q] : rv[q + half];
+      const float keep = up ? rv[q + half] : rv[q];
+      rv[q] = fminf(keep, butterfly_partner<half>(send));
+    }
+  };
+  stage(std::integral_constant<int, 16>{});
+  stage(std::integral_constant<int, 8>{});
+  stage(std::integral_constant<int, 4>{});
+  stage(std::integral_constant<int, 2>{});
+  stage(std::integral_constant<int, 1>{});
+  return rv[0];
+}
+
+// Row index (within a 64-row wave sub-tile) whose minimum transpose_min32 leaves in
+// lane (lr, lh): value index k = lr of the 32 values (mb, v) = (k / 16, k % 16).
+__device__ inline int transposed_row(int lr, int lh) {
+  return (lr >> 4) * 32 + ((lr & 15) >> 2) * 8 + lh * 4 + (lr & 3);
+}
+
+// Workspace: norms (n*p fp32) | row scales (n*p fp32) | minima bits (n*p x n uint32).
+struct Workspace {
+  float* norms;
+  float* inv;
+  uint32_t* minbits;
+};
+
+inline size_t workspace_bytes(long long n, long long p) {
+  const long long rows = n * p;
+  return 2 * align_up((size_t)rows * 4, 256) + align_up((size_t)rows * n * 4, 256);
+}
+
+inline Workspace carve(void* ws, long long n, long long p) {
+  const long long rows = n * p;
+  char* base = static_cast<char*>(ws);
+  Workspace w;
+  w.norms = reinterpret_cast<float*>(base);
+  w.inv = reinterpret_cast<float*>(base + align_up((size_t)rows * 4, 256));
+  w.minbits = reinterpret_cast<uint32_t*>(base + 2 * align_up((size_t)rows * 4, 256));
+  return w;
+}
+
+// Trimmed rank means over the minima (defined in msm.hip, shared by both engines).
+int run_rank(int n, int p, int a, int b, double* scores, const Workspace& w, hipStream_t s);
+
+}  // namespace msm
+}  // namespace musc

@@ -1,0 +1,459 @@
+// MSM pair minima with fp32-accurate dot products formed on the fp16 matrix cores.
+//
+// Same contract as msm_pair_min_kernel (msm.hip), i.e. models/modules/_MSM.py:10-30:
+// per (patch, other image) the minimum squared distance ||a||^2 + ||b||^2 - 2 a.b,
+// clamped at 0, merged with atomicMin on the float bits; the trimmed rank means are
+// shared with the fp32 engine.  Only the dot products are formed differently.
+//
+// Split (Ootomo & Yokota, "Recovering single precision accuracy from Tensor Cores
+// while surpassing the FP32 theoretical peak performance", IJHPCA 2022, restated for
+// fp16 MFMA): every row is L2-normalised and scaled by 2^kScaleShift (so its entries
+// lie in fp16's normal range), then split as v = hi + lo with hi = fp16(v) and
+// lo = fp16(v - hi).  a.b is accumulated in fp32 as hi_a.hi_b + hi_a.lo_b + lo_a.hi_b;
+// the dropped lo_a.lo_b term and the rounding of lo are below 2^-22 |a||b|, the
+// order of fp32's own accumulation error, and a per-row scale restores the units.
+// v_mfma_f32_32x32x16_f16 runs 16x the fp32 MFMA rate, so the three products cost
+// 3/16 of one fp32 product.
+//
+// MI355X layout
+//   split array   per row, per 32-channel block: hi[32] | lo[32] fp16 (128 bytes,
+//                 one cache line per row and pipeline stage); channels padded to a
+//                 multiple of 32 with zeros.
+//   pair kernel   256 x 256 tiles of the upper triangle (symmetric reuse, bands of
+//                 8 tile rows, XCD-grouped), 8 waves each owning 64 x 128.  Stages
+//                 of 32 channels go straight from global memory into LDS
+//                 (global_load_lds_dwordx4: lane l of a load lands at base + 16 l, so
+//                 one load fills 8 rows of 128 bytes), double-buffered, one barrier
+//                 per stage, no staging registers.  The 16-byte segment s of staged
+//                 row r sits at position s ^ (r & 7), which makes the MFMA operand
+//                 reads (8 consecutive rows, one segment) hit 8 distinct bank groups.
+//                 Register epilogues as in the fp32 kernel (one image segment per
+//                 dimension, or two when the tile straddles an image boundary:
+//                 p >= 256 is required).
+#include <hip/hip_fp16.h>
+
+#include "msm_common.hpp"
+
+namespace musc {
+namespace msm {
+namespace split {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+
+constexpr int TM = 256;                      // tile rows = tile columns
+constexpr int KB = 32;                       // channels per stage (each of hi and lo)
+constexpr int ROWB = 128;                    // LDS row: hi[32] lo[32] fp16, swizzled segments
+constexpr int THREADS = 512;                 // 8 waves: 4 (rows) x 2 (columns)
+constexpr int kStageBytes = 2 * TM * ROWB;   // A rows then B rows
+constexpr int kScaleShift = 10;              // normalised rows are scaled by 2^10
+constexpr int kLoads = 2 * TM / 8 / (THREADS / kWave);  // direct loads (8 rows each) per wave per stage
+
+static_assert(kLoads == 8, "stage loads: 512 rows, 8 per load, over 8 waves");
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// ---------------------------------------------------------------------------
+// Prepare: one wave per row.  norms[] exactly as msm_norms_kernel; inv[] holds the
+// epilogue's per-row scale of the split dot product.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void split_prepare_kernel(const float* __restrict__ z, int rows, int c, int nkb,
+                                                            int normalize, float* __restrict__ norms,
+                                                            float* __restrict__ inv, _Float16* __restrict__ hl) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const long long row = (long long)blockIdx.x * (blockDim.x / kWave) + wave;
+  if (row >= rows) return;
+  const float* src = z + row * (long long)c;
+  const double acc = row_sumsq(src, c, lane);
+  const double unit = ldexp(1.0, -kScaleShift);
+  if (lane == 0) {
+    if (normalize) {
+      const double r = 1.0 / sqrt(acc);
+      norms[row] = (float)(acc * r * r);
+      inv[row] = (float)unit;
+    } else {
+      norms[row] = (float)acc;
+      inv[row] = (float)(sqrt(acc) * unit);
+    }
+  }
+  const double sc = acc > 0.0 ? ldexp(1.0 / sqrt(acc), kScaleShift) : 0.0;
+  _Float16* dst = hl + row * (long long)nkb * 64;
+  const int cp = nkb * KB;
+  for (int k = lane; k < cp; k += kWave) {
+    const double v = k < c ? (double)src[k] * sc : 0.0;
+    const _Float16 hi = (_Float16)(float)v;
+    const _Float16 lo = (_Float16)(float)(v - (double)(float)hi);
+    dst[(k / KB) * 64 + (k % KB)] = hi;
+    dst[(k / KB) * 64 + KB + (k % KB)] = lo;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pair minima.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* __restrict__ hl,
+                                                               const float* __restrict__ norms,
+                                                               const float* __restrict__ inv,
+                                                               uint32_t* __restrict__ minbits, int rows, int n, int p,
+                                                               int nkb, int T, long long ntiles) {
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * kStageBytes];
+  __shared__ __attribute__((aligned(16))) float s_rnorm[TM];
+  __shared__ __attribute__((aligned(16))) float s_cnorm[TM];
+  __shared__ __attribute__((aligned(16))) float s_rinv[TM];
+  __shared__ __attribute__((aligned(16))) float s_cinv[TM];
+  __shared__ __attribute__((aligned(16))) int s_rimg[TM];
+  __shared__ int s_cimg[TM];
+
+  const long long w = xcd_logical_id(blockIdx.x, gridDim.x);
+  if (w >= ntiles) return;
+  const int2 tile = decode_tile(w, T);
+  const int row0 = tile.x * TM, col0 = tile.y * TM;
+  const int rlast = min(row0 + TM, rows) - 1, clast = min(col0 + TM, rows) - 1;
+  const int rimg0 = row0 / p, cimg0 = col0 / p;
+  const bool simple = (row0 + TM <= rows) && (col0 + TM <= rows) && (rlast / p == rimg0) && (clast / p == cimg0);
+  if (simple && rimg0 == cimg0) return;
+
+  const int t = threadIdx.x;
+  if (t < TM) {
+    const int r = row0 + t;
+    s_rnorm[t] = r < rows ? norms[r] : 0.f;
+    s_rinv[t] = r < rows ? inv[r] : 0.f;
+    s_rimg[t] = r < rows ? r / p : n;  // n marks "no image" (padding)
+  } else {
+    const int j = t - TM, cc = col0 + j;
+    s_cnorm[j] = cc < rows ? norms[cc] : 0.f;
+    s_cinv[j] = cc < rows ? inv[cc] : 0.f;
+    s_cimg[j] = cc < rows ? cc / p : n;
+  }
+
+  const int wave = t / kWave, lane = t % kWave;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lr = lane & 31, lh = lane >> 5;
+
+  floatx16 acc[2][4];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.f;
+
+  // Loads: wave wv fills staged rows wv*64 .. wv*64 + 63, eight per load; staged rows
+  // 0..255 are tile rows (A), 256..511 tile columns (B).  Lane l of a load carries
+  // row R = R0 + l/8, LDS position l % 8, i.e. segment (l % 8) ^ (R & 7) = (l % 8) ^
+  // (l / 8).  Padded rows re-read the last row (masked in the epilogue).
+  const int lrow8 = lane >> 3, lseg = (lane & 7) ^ lrow8;
+  auto issue = [&](int kb, int buf) {
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int R0 = wave * 64 + i * 8;
+      const int R = R0 + lrow8;
+      const int grow = R < TM ? min(row0 + R, rows - 1) : min(col0 + R - TM, rows - 1);
+      __builtin_amdgcn_global_load_lds(hl + ((long long)grow * nkb + kb) * 64 + lseg * 8,
+                                       (lds_void*)(smem + buf * kStageBytes + R0 * ROWB), 16, 0, 0);
+    }
+  };
+  // operand of staged row r, segment sg (hi: 0..3, lo: 4..7); r & 7 == lr & 7 here
+  const int sw = lr & 7;
+  auto compute = [&](int buf) {
+    const unsigned char* As = smem + buf * kStageBytes + (wm * 64 + lr) * ROWB;
+    const unsigned char* Bs = smem + buf * kStageBytes + (TM + wn * 128 + lr) * ROWB;
+#pragma unroll
+    for (int j = 0; j < KB / 16; ++j) {
+      const int phi = ((2 * j + lh) ^ sw) * 16, plo = ((4 + 2 * j + lh) ^ sw) * 16;
+      half8 ahi[2], alo[2], bhi[4], blo[4];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        ahi[mb] = *reinterpret_cast<const half8*>(As + mb * 32 * ROWB + phi);
+        alo[mb] = *reinterpret_cast<const half8*>(As + mb * 32 * ROWB + plo);
+      }
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        bhi[nb] = *reinterpret_cast<const half8*>(Bs + nb * 32 * ROWB + phi);
+        blo[nb] = *reinterpret_cast<const half8*>(Bs + nb * 32 * ROWB + plo);
+      }
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[mb], bhi[nb], acc[mb][nb], 0, 0, 0);
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[mb], blo[nb], acc[mb][nb], 0, 0, 0);
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo[mb], bhi[nb], acc[mb][nb], 0, 0, 0);
+    }
+  };
+
+  // Stage kc lives in LDS buffer kc & 1.  Iteration kc waits for its own loads of
+  // stage kc, then the barrier makes every wave's loads visible and guarantees that
+  // buffer (kc + 1) & 1 is no longer read (compute(kc - 1) is done everywhere), so
+  // the loads of stage kc + 1 go out before compute(kc) and have its duration to land.
+  issue(0, 0);
+  for (int kc = 0; kc < nkb; ++kc) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (kc + 1 < nkb) issue(kc + 1, (kc + 1) & 1);
+    compute(kc & 1);
+  }
+
+  // Epilogue.  Lane (lr, lh) of wave (wm, wn) holds, for mb < 2, nb < 4, v < 16, the
+  // dot of tile row wm*64 + mb*32 + (v/4)*8 + lh*4 + v%4 with tile column
+  // wn*128 + nb*32 + lr.
+  const float inf = __int_as_float(kInfBits);
+  const int rA = rimg0, cA = cimg0;
+  float d2[2][4][16];
+  bool rowB[2][16];  // row lies in image rA + 1 (two-segment tiles)
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int i0 = wm * 64 + mb * 32 + g * 8 + lh * 4;
+      const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[i0]);
+      const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[i0]);
+      const int4 rim = *reinterpret_cast<const int4*>(&s_rimg[i0]);
+      const float rv[4] = {rn.x, rn.y, rn.z, rn.w};
+      const float rs[4] = {-2.f * ri.x, -2.f * ri.y, -2.f * ri.z, -2.f * ri.w};
+      const int rimg[4] = {rim.x, rim.y, rim.z, rim.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rowB[mb][g * 4 + e] = rimg[e] != rA;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        const int j = wn * 128 + nb * 32 + lr;
+        const float cn = s_cnorm[j];
+        const float ci = s_cinv[j];
+        const int cimg = s_cimg[j];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float v = fmaxf(fmaf(rs[e] * ci, acc[mb][nb][g * 4 + e], rv[e] + cn), 0.f);
+          const bool masked = !simple && (rimg[e] == cimg || rimg[e] == n || cimg == n);
+          d2[mb][nb][g * 4 + e] = masked ? inf : v;
+        }
+      }
+    }
+
+  if (simple) {
+    // column minima over this wave's 64 rows; the two lane halves then split the
+    // column blocks: half lh keeps blocks 2q + lh (q = 0, 1)
+    float cmin[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      float m = d2[0][nb][0];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) m = fminf(m, d2[mb][nb][v]);
+      cmin[nb] = m;
+    }
+    float cm[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float send = lh ? cmin[2 * q] : cmin[2 * q + 1];
+      const float keep = lh ? cmin[2 * q + 1] : cmin[2 * q];
+      cm[q] = fminf(keep, __shfl_xor(send, 32, kWave));
+    }
+    // row minima over this wave's 128 columns: in-lane over nb, then the transposing
+    // butterfly over the 32 lanes of each half
+    float rv[32];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        rv[mb * 16 + v] = fminf(fminf(d2[mb][0][v], d2[mb][1][v]), fminf(d2[mb][2][v], d2[mb][3][v]));
+    transpose_min32(rv, lr);
+    __syncthreads();  // operand buffers are no longer read
+    float* s_cmin = reinterpret_cast<float*>(smem);  // [4 (wm)][TM]
+    float* s_rmin = s_cmin + 4 * TM;                  // [2 (wn)][TM]
+#pragma unroll
+    for (int q = 0; q < 2; ++q) s_cmin[wm * TM + wn * 128 + (2 * q + lh) * 32 + lr] = cm[q];
+    s_rmin[wn * TM + wm * 64 + transposed_row(lr, lh)] = rv[0];
+    __syncthreads();
+    if (t < TM) {
+      const float m = fminf(s_rmin[t], s_rmin[TM + t]);
+      atomicMin(minbits + (long long)(row0 + t) * n + cA, __float_as_uint(m));
+    } else {
+      const int j = t - TM;
+      const float m = fminf(fminf(s_cmin[j], s_cmin[TM + j]), fminf(s_cmin[2 * TM + j], s_cmin[3 * TM + j]));
+      atomicMin(minbits + (long long)(col0 + j) * n + rA, __float_as_uint(m));
+    }
+    return;
+  }
+
+  // Two image segments per dimension (rows: rA, rA + 1; columns: cA, cA + 1);
+  // same-image and padding pairs are +inf already.
+  float cminA[4], cminB[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+    float a = inf, b = inf;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float x = d2[mb][nb][v];
+        a = rowB[mb][v] ? a : fminf(a, x);
+        b = rowB[mb][v] ? fminf(b, x) : b;
+      }
+    cminA[nb] = a;
+    cminB[nb] = b;
+  }
+  float cmA[2], cmB[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const float sendA = lh ? cminA[2 * q] : cminA[2 * q + 1], keepA = lh ? cminA[2 * q + 1] : cminA[2 * q];
+    const float sendB = lh ? cminB[2 * q] : cminB[2 * q + 1], keepB = lh ? cminB[2 * q + 1] : cminB[2 * q];
+    cmA[q] = fminf(keepA, __shfl_xor(sendA, 32, kWave));
+    cmB[q] = fminf(keepB, __shfl_xor(sendB, 32, kWave));
+  }
+  bool colB[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) colB[nb] = s_cimg[wn * 128 + nb * 32 + lr] != cA;
+  float rowminA, rowminB;
+  {
+    float rv[32];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        float m = inf;
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) m = fminf(m, colB[nb] ? inf : d2[mb][nb][v]);
+        rv[mb * 16 + v] = m;
+      }
+    rowminA = transpose_min32(rv, lr);
+  }
+  {
+    float rv[32];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        float m = inf;
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) m = fminf(m, colB[nb] ? d2[mb][nb][v] : inf);
+        rv[mb * 16 + v] = m;
+      }
+    rowminB = transpose_min32(rv, lr);
+  }
+  __syncthreads();  // operand buffers are no longer read
+  float* s_cminA = reinterpret_cast<float*>(smem);  // [4 (wm)][TM]
+  float* s_cminB = s_cminA + 4 * TM;
+  float* s_rminA = s_cminB + 4 * TM;                 // [2 (wn)][TM]
+  float* s_rminB = s_rminA + 2 * TM;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    s_cminA[wm * TM + wn * 128 + (2 * q + lh) * 32 + lr] = cmA[q];
+    s_cminB[wm * TM + wn * 128 + (2 * q + lh) * 32 + lr] = cmB[q];
+  }
+  const int rk = wm * 64 + transposed_row(lr, lh);
+  s_rminA[wn * TM + rk] = rowminA;
+  s_rminB[wn * TM + rk] = rowminB;
+  __syncthreads();
+  if (t < TM) {
+    const int r = row0 + t;
+    if (r < rows) {
+      const float a = fminf(s_rminA[t], s_rminA[TM + t]);
+      const float b = fminf(s_rminB[t], s_rminB[TM + t]);
+      if (a < inf) atomicMin(minbits + (long long)r * n + cA, __float_as_uint(a));
+      if (b < inf) atomicMin(minbits + (long long)r * n + cA + 1, __float_as_uint(b));
+    }
+  } else {
+    const int j = t - TM;
+    const int cc = col0 + j;
+    if (cc < rows) {
+      const float a = fminf(fminf(s_cminA[j], s_cminA[TM + j]), fminf(s_cminA[2 * TM + j], s_cminA[3 * TM + j]));
+      const float b = fminf(fminf(s_cminB[j], s_cminB[TM + j]), fminf(s_cminB[2 * TM + j], s_cminB[3 * TM + j]));
+      if (a < inf) atomicMin(minbits + (long long)cc * n + rA, __float_as_uint(a));
+      if (b < inf) atomicMin(minbits + (long long)cc * n + rA + 1, __float_as_uint(b));
+    }
+  }
+}
+
+inline int nkb_of(int c) { return (c + KB - 1) / KB; }
+
+inline size_t split_array_bytes(long long rows, int c) { return align_up((size_t)rows * nkb_of(c) * 64 * 2, 256); }
+
+inline size_t workspace_bytes(long long n, long long p, int c) {
+  return msm::workspace_bytes(n, p) + split_array_bytes(n * p, c);
+}
+
+inline _Float16* split_array(void* ws, long long n, long long p) {
+  return reinterpret_cast<_Float16*>(static_cast<char*>(ws) + msm::workspace_bytes(n, p));
+}
+
+inline int validate(int n, int p, int c, void* ws, size_t ws_bytes) {
+  if (n < 2 || p < 1 || c < 1) return MUSC_ERR_INVALID_ARG;
+  const long long rows = (long long)n * p;
+  if (rows > (1LL << 30) || n > 4096) return MUSC_ERR_UNSUPPORTED;
+  if (!ws || ws_bytes < workspace_bytes(n, p, c)) return MUSC_ERR_WORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0) return MUSC_ERR_INVALID_ARG;
+  return MUSC_OK;
+}
+
+inline void run_prepare(const float* z, int n, int p, int c, int normalize, void* ws, hipStream_t s) {
+  const long long rows = (long long)n * p;
+  const Workspace w = carve(ws, n, p);
+  hipLaunchKernelGGL(split_prepare_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, z, (int)rows, c,
+                     nkb_of(c), normalize, w.norms, w.inv, split_array(ws, n, p));
+  launch_fill_u32(w.minbits, (size_t)rows * n, kInfBits, s);
+}
+
+inline int run_pairs(int n, int p, int c, void* ws, hipStream_t s) {
+  if (p < TM) return MUSC_ERR_UNSUPPORTED;  // the two-segment epilogue needs p >= 256
+  const long long rows = (long long)n * p;
+  const long long T = (rows + TM - 1) / TM;
+  const long long ntiles = total_tiles(T);
+  const long long grid = (ntiles + kXcds - 1) / kXcds * kXcds;
+  if (grid > 0x7fffffffLL) return MUSC_ERR_UNSUPPORTED;
+  const Workspace w = carve(ws, n, p);
+  hipLaunchKernelGGL(split_pair_kernel, dim3((unsigned)grid), dim3(THREADS), 0, s, split_array(ws, n, p), w.norms,
+                     w.inv, w.minbits, (int)rows, n, p, nkb_of(c), (int)T, ntiles);
+  return check_launch();
+}
+
+}  // namespace split
+}  // namespace msm
+}  // namespace musc
+
+using namespace musc;
+
+extern "C" int musc_msm_split_workspace_bytes(int n, int p, int c, size_t* out) {
+  if (!out || n < 2 || p < 1 || c < 1) return MUSC_ERR_INVALID_ARG;
+  *out = msm::split::workspace_bytes(n, p, c);
+  return MUSC_OK;
+}
+
+extern "C" int musc_msm_split_prepare_f32(const float* z, int n, int p, int c, int flags, void* workspace,
+                                          size_t workspace_bytes, hipStream_t stream) {
+  int rc = msm::split::validate(n, p, c, workspace, workspace_bytes);
+  if (rc) return rc;
+  if (!z || (flags & ~MUSC_MSM_NORMALIZE_ROWS)) return MUSC_ERR_INVALID_ARG;
+  if ((c & 3) == 0 && (reinterpret_cast<uintptr_t>(z) & 15) != 0) return MUSC_ERR_INVALID_ARG;
+  msm::split::run_prepare(z, n, p, c, (flags & MUSC_MSM_NORMALIZE_ROWS) ? 1 : 0, workspace, stream);
+  return check_launch();
+}
+
+extern "C" int musc_msm_split_pair_minima(int n, int p, int c, void* workspace, size_t workspace_bytes,
+                                          hipStream_t stream) {
+  int rc = msm::split::validate(n, p, c, workspace, workspace_bytes);
+  if (rc) return rc;
+  return msm::split::run_pairs(n, p, c, workspace, stream);
+}
+
+extern "C" int musc_msm_split_scores_f32(const float* z, int n, int p, int c, int rank_lo, int rank_hi, int flags,
+                                         double* scores, void* workspace, size_t workspace_bytes,
+                                         hipStream_t stream) {
+  int rc = msm::split::validate(n, p, c, workspace, workspace_bytes);
+  if (rc) return rc;
+  if (!z || !scores || rank_lo < 0 || rank_lo >= rank_hi || rank_hi > n - 1) return MUSC_ERR_INVALID_ARG;
+  if (flags & ~MUSC_MSM_NORMALIZE_ROWS) return MUSC_ERR_INVALID_ARG;
+  if ((c & 3) == 0 && (reinterpret_cast<uintptr_t>(z) & 15) != 0) return MUSC_ERR_INVALID_ARG;
+  if (p < msm::split::TM) return MUSC_ERR_UNSUPPORTED;
+  msm::split::run_prepare(z, n, p, c, (flags & MUSC_MSM_NORMALIZE_ROWS) ? 1 : 0, workspace, stream);
+  rc = msm::split::run_pairs(n, p, c, workspace, stream);
+  if (rc) return rc;
+  return msm::run_rank(n, p, rank_lo, rank_hi, scores, msm::carve(workspace, n, p), stream);
+}

@@ -50,6 +50,10 @@ SIGNATURES = {
     'musc_msm_prepare_f32': (_i, [_vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     'musc_msm_pair_minima_f32': (_i, [_vp, _i, _i, _i, _vp, _sz, _vp]),
     'musc_msm_rank_f32': (_i, [_i, _i, _i, _i, _vp, _vp, _sz, _vp]),
+    'musc_msm_split_workspace_bytes': (_i, [_i, _i, _i, ctypes.POINTER(_sz)]),
+    'musc_msm_split_prepare_f32': (_i, [_vp, _i, _i, _i, _i, _vp, _sz, _vp]),
+    'musc_msm_split_pair_minima': (_i, [_i, _i, _i, _vp, _sz, _vp]),
+    'musc_msm_split_scores_f32': (_i, [_vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
     'musc_lnamd_workspace_bytes': (_i, [_i, _i, ctypes.POINTER(_sz)]),
     'musc_lnamd_f32': (_i, [_vp, _i, _i, _i, _i, _i, _i, _vp, _i, _f, _i, _vp, _i, _vp, _sz, _vp]),
     'musc_lnamd_pooled_f32': (_i, [_vp, _i, _i, _i, _i, _i, _i, _vp, _i, _f, _i, _i, _vp, _i, _vp, _sz, _vp]),

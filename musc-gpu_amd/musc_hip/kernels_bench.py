@@ -1,6 +1,6 @@
 """Per-kernel micro-benchmarks of libmusc_hip on one GPU (used for rocprofv3 runs).
 
-    python musc-gpu_amd/musc_hip/kernels_bench.py msm [--n 83 --p 1369 --c 1024 --iters 3]
+    python musc-gpu_amd/musc_hip/kernels_bench.py msm [--n 83 --p 1369 --c 1024 --iters 3 --engine fp32|split16]
     python musc-gpu_amd/musc_hip/kernels_bench.py lnamd [--n 83 --layers 4 --iters 3]
     python musc-gpu_amd/musc_hip/kernels_bench.py attention [--dtype fp32|fp16 --blocks 24]
     python musc-gpu_amd/musc_hip/kernels_bench.py copy [--mib 1024 --iters 3]
@@ -43,19 +43,28 @@ def _events():
 def bench_msm(args):
     dev = torch.device('cuda:0')
     n, p, c = args.n, args.p, args.c
+    engine = args.engine
     z = synthetic.msm_features(n, p, c, seed=42).to(dev)
     a, b = _MSM_hip.rank_window(n)
-    ws = rt.workspace(_MSM_hip.workspace_bytes(n, p, c), dev)
+    _MSM_hip.check_engine(engine, p)
+    ws = rt.workspace(_MSM_hip.workspace_bytes(n, p, c, engine), dev)
     scores = torch.empty((n, p), dtype=torch.float64, device=dev)
     lib, s = rt.library(), rt.stream(dev)
     t = {'prepare': [], 'pairs': [], 'rank': []}
     for it in range(args.iters + 1):
         evs = [_events() for _ in range(3)]
         evs[0][0].record()
-        rt.check(lib.musc_msm_prepare_f32(z.data_ptr(), n, p, c, 0, ws.data_ptr(), ws.numel(), s), 'prepare')
+        if engine == 'split16':
+            rt.check(lib.musc_msm_split_prepare_f32(z.data_ptr(), n, p, c, 0, ws.data_ptr(), ws.numel(), s),
+                     'prepare')
+        else:
+            rt.check(lib.musc_msm_prepare_f32(z.data_ptr(), n, p, c, 0, ws.data_ptr(), ws.numel(), s), 'prepare')
         evs[0][1].record()
         evs[1][0].record()
-        rt.check(lib.musc_msm_pair_minima_f32(z.data_ptr(), n, p, c, ws.data_ptr(), ws.numel(), s), 'pairs')
+        if engine == 'split16':
+            rt.check(lib.musc_msm_split_pair_minima(n, p, c, ws.data_ptr(), ws.numel(), s), 'pairs')
+        else:
+            rt.check(lib.musc_msm_pair_minima_f32(z.data_ptr(), n, p, c, ws.data_ptr(), ws.numel(), s), 'pairs')
         evs[1][1].record()
         evs[2][0].record()
         rt.check(lib.musc_msm_rank_f32(n, p, a, b, scores.data_ptr(), ws.data_ptr(), ws.numel(), s), 'rank')
@@ -68,8 +77,16 @@ def bench_msm(args):
     avg = {k: sum(v) / len(v) for k, v in t.items()}
     flop = float(c) * p * p * n * (n - 1)
     tf = flop / (avg['pairs'] / 1e3) / 1e12
-    return {'kernel': 'msm', 'n': n, 'p': p, 'c': c, 'avg_ms': avg, 'pair_flop': flop, 'pair_tflops': tf,
-            'pair_frac_fp32_mfma_peak': tf / FP32_MFMA_TFLOPS}
+    res = {'kernel': 'msm', 'engine': engine, 'n': n, 'p': p, 'c': c, 'avg_ms': avg, 'pair_flop': flop,
+           'pair_tflops': tf}
+    if engine == 'split16':
+        # three fp16 MFMA products per fp32 dot product: the fp16 matrix-core work is 3x the
+        # algorithmic FLOP; tf is the fp32-equivalent rate
+        res['pair_fp16_mfma_tflops'] = 3 * tf
+        res['pair_frac_fp16_mfma_peak'] = 3 * tf / FP16_MFMA_TFLOPS
+    else:
+        res['pair_frac_fp32_mfma_peak'] = tf / FP32_MFMA_TFLOPS
+    return res
 
 
 def bench_lnamd(args):
@@ -289,6 +306,7 @@ def main():
     ap.add_argument('--blocks', type=int, default=24)
     ap.add_argument('--mib', type=int, default=1024)
     ap.add_argument('--iters', type=int, default=3)
+    ap.add_argument('--engine', choices=['fp32', 'split16'], default='fp32', help='MSM dot-product engine')
     args = ap.parse_args()
     table = {'msm': bench_msm, 'lnamd': bench_lnamd, 'super_fast': bench_super_fast, 'attention': bench_attention,
              'copy': bench_copy, 'e2e': bench_e2e, 'mfma_peak': bench_mfma_peak, 'hbm': bench_hbm}

@@ -43,13 +43,14 @@ def lnamd_pools(tokens: list[torch.Tensor], r_list: list[int], pool_grid: int | 
 
 
 def msm_all(pools: torch.Tensor, topmin_min: float = 0, topmin_max: float = 0.3,
-            pair_events: list | None = None, normalize_rows: bool = True) -> torch.Tensor:
+            pair_events: list | None = None, normalize_rows: bool = True, engine: str = 'fp32') -> torch.Tensor:
     """(R, L, N, P) float64 MSM maps of every (radius, layer) pool.
 
     Runs the three MSM stages explicitly (prepare, pair minima, rank) so that a
     caller can pass `pair_events`, a list that receives one (start, end)
     torch.cuda.Event pair recorded around each pair-minima kernel on the stream
-    it runs on.
+    it runs on.  `engine` selects how the dot products are formed ('fp32' or
+    'split16', see _MSM_hip).
     """
     r, l, n, p, c = pools.shape
     a, b = _MSM_hip.rank_window(n, topmin_min, topmin_max)
@@ -57,21 +58,31 @@ def msm_all(pools: torch.Tensor, topmin_min: float = 0, topmin_max: float = 0.3,
         raise ValueError('Require valid nonempty trimmed ranks 0<=a<b<=N-1.')
     if pools.dtype != torch.float32 or not pools.is_contiguous():
         raise ValueError('pools must be a contiguous fp32 (R, L, N, P, C) tensor')
+    _MSM_hip.check_engine(engine, p)
     scores = torch.empty((r, l, n, p), dtype=torch.float64, device=pools.device)
-    ws = rt.workspace(_MSM_hip.workspace_bytes(n, p, c), pools.device)
+    ws = rt.workspace(_MSM_hip.workspace_bytes(n, p, c, engine), pools.device)
     lib = rt.library()
     s = rt.stream(pools.device)
     flags = rt.MSM_NORMALIZE_ROWS if normalize_rows else 0
+    split = engine == 'split16'
     for ri in range(r):
         for li in range(l):
             z = pools[ri, li]
-            rt.check(lib.musc_msm_prepare_f32(z.data_ptr(), n, p, c, flags, ws.data_ptr(), ws.numel(), s),
-                     'musc_msm_prepare_f32')
+            if split:
+                rt.check(lib.musc_msm_split_prepare_f32(z.data_ptr(), n, p, c, flags, ws.data_ptr(), ws.numel(), s),
+                         'musc_msm_split_prepare_f32')
+            else:
+                rt.check(lib.musc_msm_prepare_f32(z.data_ptr(), n, p, c, flags, ws.data_ptr(), ws.numel(), s),
+                         'musc_msm_prepare_f32')
             if pair_events is not None:
                 ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                 ev[0].record()
-            rt.check(lib.musc_msm_pair_minima_f32(z.data_ptr(), n, p, c, ws.data_ptr(), ws.numel(), s),
-                     'musc_msm_pair_minima_f32')
+            if split:
+                rt.check(lib.musc_msm_split_pair_minima(n, p, c, ws.data_ptr(), ws.numel(), s),
+                         'musc_msm_split_pair_minima')
+            else:
+                rt.check(lib.musc_msm_pair_minima_f32(z.data_ptr(), n, p, c, ws.data_ptr(), ws.numel(), s),
+                         'musc_msm_pair_minima_f32')
             if pair_events is not None:
                 ev[1].record()
                 pair_events.append(ev)
@@ -82,13 +93,14 @@ def msm_all(pools: torch.Tensor, topmin_min: float = 0, topmin_max: float = 0.3,
 
 def score_pool(tokens: list[torch.Tensor], r_list=(1, 3, 5), image_size: int = 518, topmin_min: float = 0,
                topmin_max: float = 0.3, want_maps: bool = True, timing: dict | None = None,
-               pool_grid: int | None = None):
+               pool_grid: int | None = None, msm_engine: str = 'fp32'):
     """Tokens (list over layers of (N, 1+P, C) GPU tensors) -> (maps (N,1,S,S) f64, image scores (N,) f64).
 
     `timing`, if given, receives torch.cuda.Event pairs: timing['lnamd'] (one
     pair around the LNAMD launch) and timing['pairs'] (one per MSM pair kernel).
     `pool_grid` (the super_fast profile: 28) adaptively pools every patch grid to
     pool_grid x pool_grid before scoring (models/modules/_super_fast.py:17-27).
+    `msm_engine` selects the MSM dot-product engine ('fp32' or 'split16').
     """
     lnamd_ev = None
     if timing is not None:
@@ -99,7 +111,7 @@ def score_pool(tokens: list[torch.Tensor], r_list=(1, 3, 5), image_size: int = 5
         lnamd_ev[1].record()
         timing.setdefault('lnamd', []).append(lnamd_ev)
     scores = msm_all(pools, topmin_min, topmin_max,
-                     pair_events=timing.setdefault('pairs', []) if timing is not None else None)
+                     pair_events=timing.setdefault('pairs', []) if timing is not None else None, engine=msm_engine)
     del pools
     return _epilogue_hip.maps_and_scores(scores, image_size, want_maps=want_maps)
 

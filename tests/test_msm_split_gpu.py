@@ -1,0 +1,139 @@
+"""Split MSM engine (fp32 dot products from three fp16 MFMA products) vs the oracle.
+
+Same gate as the fp32 engine: 2e-5 absolute on scores (tools/benchmark_support.py:11).
+The per-(patch, image) minima are also checked directly against the float64 brute force.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import msm as om
+from musc_hip import _MSM_hip, pipeline, synthetic
+from musc_hip import _runtime as rt
+
+pytestmark = pytest.mark.gpu
+ATOL = 2e-5  # tools/benchmark_support.py:11
+
+
+def _split(z, **kw):
+    return _MSM_hip.MSM(z, engine='split16', **kw)
+
+
+# p = 256: tiles aligned with images; 257/300/400/1369: tiles straddling an image boundary
+# (two-segment epilogue) and a padded last tile row; c % 32 != 0: zero-padded channel blocks
+@pytest.mark.parametrize('n,p,c', [(5, 256, 64), (5, 257, 33), (6, 300, 1024), (5, 1369, 100), (9, 400, 7),
+                                   (7, 512, 32)])
+def test_random_shapes_vs_oracles(device, n, p, c):
+    torch.manual_seed(n * 1000 + p)
+    z = torch.nn.functional.normalize(torch.randn((n, p, c)), dim=-1)
+    got = _split(z.to(device)).cpu().numpy()
+    ref_t = om.MSM(z).numpy()
+    ref_64 = oracle.msm_scores_f64_c(z.numpy(), *om.rank_window(n))
+    np.testing.assert_allclose(got, ref_t, rtol=0, atol=ATOL)
+    np.testing.assert_allclose(got, ref_64, rtol=0, atol=ATOL)
+
+
+def _split_minima(z: torch.Tensor, normalize: bool) -> np.ndarray:
+    """Squared per-(row, image) minima left by the split pair kernel in its workspace."""
+    n, p, c = z.shape
+    lib = rt.library()
+    ws = rt.workspace(_MSM_hip.workspace_bytes(n, p, c, 'split16'), z.device)
+    s = rt.stream(z.device)
+    flags = rt.MSM_NORMALIZE_ROWS if normalize else 0
+    rt.check(lib.musc_msm_split_prepare_f32(z.data_ptr(), n, p, c, flags, ws.data_ptr(), ws.numel(), s), 'prepare')
+    rt.check(lib.musc_msm_split_pair_minima(n, p, c, ws.data_ptr(), ws.numel(), s), 'pairs')
+    torch.cuda.synchronize()
+    rows = n * p
+    off = 2 * ((rows * 4 + 255) // 256 * 256)
+    bits = ws[off:off + rows * n * 4].view(torch.int32).cpu().numpy().view(np.uint32)
+    return bits.view(np.float32).reshape(rows, n)
+
+
+def test_minima_vs_f64_bruteforce(device):
+    torch.manual_seed(21)
+    z = torch.nn.functional.normalize(torch.randn((5, 300, 96)), dim=-1)
+    got = _split_minima(z.to(device), normalize=False)
+    ref = oracle.msm_nearest_f64_c(z.numpy()) ** 2
+    fin = np.isfinite(ref)
+    assert np.isinf(got[~fin]).all(), 'own-image entries must stay +inf'
+    # squared distances of unit vectors: fp32-level agreement (|d^2| <= 4)
+    np.testing.assert_allclose(got[fin], ref[fin], rtol=0, atol=2e-6)
+
+
+def test_config1_plumbing_kernel_level(device):
+    z = synthetic.msm_features(8, 1369, 1024, seed=42)
+    zd = z.to(device)
+    got = _split(zd).cpu().numpy()
+    fp32 = _MSM_hip.MSM(zd).cpu().numpy()
+    ref = om.MSM(z).numpy()
+    err, diff = np.abs(got - ref).max(), np.abs(got - fp32).max()
+    print(f'config1 split engine: max abs err vs oracle {err:.3e}, vs fp32 engine {diff:.3e}', flush=True)
+    assert err <= ATOL
+
+
+def test_default_pool_sampled_queries(device):
+    toks = synthetic.pool_tokens(83, layers=1, seed=42)[0]
+    z = toks[:, 1:, :].contiguous()
+    got = _split(z.to(device)).cpu().numpy()
+    for i in (0, 41, 82):
+        ref = om.compute_scores_fast(z, i).double().numpy()
+        err = np.abs(got[i] - ref).max()
+        print(f'config2 split engine, query image {i}: max abs err {err:.3e}', flush=True)
+        assert err <= ATOL
+
+
+def test_super_fast_shape_deterministic_and_sampled(device):
+    z = synthetic.msm_features(83, 784, 1024, seed=7).to(device)
+    a = _split(z)
+    b = _split(z)
+    assert torch.equal(a, b), 'split engine must be bitwise deterministic'
+    perm = torch.randperm(83, generator=torch.Generator().manual_seed(1)).to(device)
+    c = _split(z[perm].contiguous())
+    assert (c - a[perm]).abs().max().item() <= 1e-6
+    zc = z.cpu()
+    for i in (5, 77):
+        ref = om.compute_scores_fast(zc, i).double().numpy()
+        assert np.abs(a[i].cpu().numpy() - ref).max() <= ATOL
+
+
+def test_normalize_rows_and_raw_rows(device):
+    torch.manual_seed(12)
+    z = torch.randn((7, 260, 96)) * 3.0 + 0.7
+    got = _split(z.to(device), normalize_rows=True).cpu().numpy()
+    ref = om.MSM(torch.nn.functional.normalize(z, dim=-1)).numpy()
+    np.testing.assert_allclose(got, ref, rtol=0, atol=ATOL)
+    # unnormalised rows: the per-row scale carries ||z|| (distances here are ~30)
+    raw = _split(z.to(device)).cpu().numpy()
+    np.testing.assert_allclose(raw, om.MSM(z).numpy(), rtol=0, atol=1e-4)
+
+
+def test_identical_images_score_near_zero(device):
+    base = torch.nn.functional.normalize(torch.randn((1, 256, 32)), dim=-1)
+    got = _split(base.repeat(6, 1, 1).to(device)).cpu().numpy()
+    assert got.max() < 1e-3
+
+
+def test_pipeline_engine_matches_fp32_engine(device):
+    toks = [t.to(device) for t in synthetic.pool_tokens(8, layers=2, seed=5)]
+    m32, i32 = pipeline.score_pool(toks, r_list=[1, 3], image_size=64)
+    m16, i16 = pipeline.score_pool(toks, r_list=[1, 3], image_size=64, msm_engine='split16')
+    assert (m16 - m32).abs().max().item() <= ATOL
+    assert (i16 - i32).abs().max().item() <= ATOL
+
+
+def test_engine_validation(device):
+    z = torch.randn((6, 100, 16), device=device)
+    with pytest.raises(ValueError, match='P >= 256'):
+        _split(z)
+    with pytest.raises(ValueError, match='Unknown MSM engine'):
+        _MSM_hip.MSM(torch.randn((6, 300, 16), device=device), engine='bf16')
+    n, p, c = 6, 100, 16
+    size = ctypes.c_size_t()
+    lib = rt.library()
+    rt.check(lib.musc_msm_split_workspace_bytes(n, p, c, ctypes.byref(size)), 'ws')
+    ws = rt.workspace(size.value, device)
+    rc = lib.musc_msm_split_pair_minima(n, p, c, ws.data_ptr(), ws.numel(), rt.stream(device))
+    assert rc == 1003  # MUSC_ERR_UNSUPPORTED: the C-ABI rejects p < 256 itself
