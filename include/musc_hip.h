@@ -288,6 +288,9 @@ int musc_activation(const void* x, void* y, int dtype, int mode, long long n, hi
  * floats).  *flop (host, may be NULL) receives the FLOP count of the launch, so
  * flop / time is the sustained fp32 MFMA rate of the device. */
 int musc_calibrate_mfma_f32(float* out, int blocks, int iters, double* flop, hipStream_t stream);
+/* The same with independent v_mfma_f32_32x32x16_f16 (the split MSM engine's
+ * instruction): the sustained fp16 MFMA rate of the device. */
+int musc_calibrate_mfma_f16(float* out, int blocks, int iters, double* flop, hipStream_t stream);
 
 /* HBM calibration (no counterpart in the reference; measurement aids).
  * musc_calibrate_hbm_stream: mode 0 reads `bytes` of src (nontemporal loads), 1 writes

@@ -33,10 +33,50 @@ __global__ __launch_bounds__(256, 2) void mfma_f32_loop(float* __restrict__ out,
   out[(long long)blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
+// fp16 counterpart: independent v_mfma_f32_32x32x16_f16 on four accumulators (the
+// instruction of the split MSM engine).
+typedef _Float16 cal_half8 __attribute__((ext_vector_type(8)));
+
+__global__ __launch_bounds__(256, 2) void mfma_f16_loop(float* __restrict__ out, int iters, float seed) {
+  floatx16 acc[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[b][v] = 0.f;
+  cal_half8 a, c;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = (_Float16)(seed + threadIdx.x * 1e-3f + i * 1e-2f);
+    c[i] = (_Float16)(seed - threadIdx.x * 1e-3f - i * 1e-2f);
+  }
+  for (int i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, c, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(c, a, acc[1], 0, 0, 0);
+      acc[2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, a, acc[2], 0, 0, 0);
+      acc[3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(c, c, acc[3], 0, 0, 0);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) s += acc[b][v];
+  out[(long long)blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
 }  // namespace cal
 }  // namespace musc
 
 using namespace musc;
+
+extern "C" int musc_calibrate_mfma_f16(float* out, int blocks, int iters, double* flop, hipStream_t stream) {
+  if (!out || blocks < 1 || iters < 1) return MUSC_ERR_INVALID_ARG;
+  if (flop) *flop = (double)blocks * 4 /* waves */ * iters * 64 /* MFMAs */ * 32768.0;
+  hipLaunchKernelGGL(cal::mfma_f16_loop, dim3(blocks), dim3(256), 0, stream, out, iters, 1.0f);
+  return check_launch();
+}
 
 extern "C" int musc_calibrate_mfma_f32(float* out, int blocks, int iters, double* flop, hipStream_t stream) {
   if (!out || blocks < 1 || iters < 1) return MUSC_ERR_INVALID_ARG;

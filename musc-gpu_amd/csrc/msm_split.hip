@@ -16,17 +16,19 @@
 // 3/16 of one fp32 product.
 //
 // MI355X layout
-//   split array   per row, per 32-channel block: hi[32] | lo[32] fp16 (128 bytes,
-//                 one cache line per row and pipeline stage); channels padded to a
-//                 multiple of 32 with zeros.
+//   split array   per row, per 16-channel block: hi[16] | lo[16] fp16 (64 bytes, one
+//                 row's share of a pipeline stage); channels padded to a multiple of
+//                 16 with zeros.
 //   pair kernel   256 x 256 tiles of the upper triangle (symmetric reuse, bands of
-//                 8 tile rows, XCD-grouped), 8 waves each owning 64 x 128.  Stages
-//                 of 32 channels go straight from global memory into LDS
-//                 (global_load_lds_dwordx4: lane l of a load lands at base + 16 l, so
-//                 one load fills 8 rows of 128 bytes), double-buffered, one barrier
-//                 per stage, no staging registers.  The 16-byte segment s of staged
-//                 row r sits at position s ^ (r & 7), which makes the MFMA operand
-//                 reads (8 consecutive rows, one segment) hit 8 distinct bank groups.
+//                 8 tile rows, XCD-grouped); a workgroup takes one 128-row half, two
+//                 workgroups share a CU, 4 waves each own 64 x 128.  Stages of 16
+//                 channels go straight from global memory into LDS
+//                 (buffer_load_dwordx4 ... lds: lane l of a load lands at base + 16 l,
+//                 so one load fills 16 rows of 64 bytes) through a 3-deep ring, loads
+//                 2 stages ahead of the MFMAs, one barrier per stage, no staging
+//                 registers.  The 16-byte segment s of staged row r sits at position
+//                 s ^ ((r >> 2) & 3), which keeps the MFMA operand reads free of bank
+//                 conflicts.
 //                 Register epilogues as in the fp32 kernel (one image segment per
 //                 dimension, or two when the tile straddles an image boundary:
 //                 p >= 256 is required).
@@ -40,17 +42,26 @@ namespace split {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 
-constexpr int TM = 256;                      // tile rows = tile columns
-constexpr int KB = 32;                       // channels per stage (each of hi and lo)
-constexpr int ROWB = 128;                    // LDS row: hi[32] lo[32] fp16, swizzled segments
-constexpr int THREADS = 512;                 // 8 waves: 4 (rows) x 2 (columns)
-constexpr int kStageBytes = 2 * TM * ROWB;   // A rows then B rows
+constexpr int TM = 256;                      // triangle tile: rows = columns
+constexpr int TR = 128;                      // tile rows per workgroup (half a triangle tile)
+constexpr int TC = 256;                      // tile columns per workgroup
+constexpr int KB = 16;                       // channels per stage (each of hi and lo)
+constexpr int ROWB = 4 * KB;                 // bytes per row and stage: hi[16] lo[16] fp16
+constexpr int NSTAGE = 3;                    // LDS ring depth: loads run NSTAGE - 1 stages ahead
+constexpr int THREADS = 256;                 // 4 waves: 2 (rows) x 2 (columns) of 64 x 128
+constexpr int kStageRows = TR + TC;          // A rows then B rows
+constexpr int kStageBytes = kStageRows * ROWB;  // 24 KB
 constexpr int kScaleShift = 10;              // normalised rows are scaled by 2^10
-constexpr int kLoads = 2 * TM / 8 / (THREADS / kWave);  // direct loads (8 rows each) per wave per stage
+constexpr int kRowsPerLoad = kWave * 16 / ROWB;                          // 16 staged rows per direct load
+constexpr int kLoads = kStageRows / kRowsPerLoad / (THREADS / kWave);    // direct loads per wave per stage
 
-static_assert(kLoads == 8, "stage loads: 512 rows, 8 per load, over 8 waves");
+static_assert(kLoads == 6, "stage loads: 384 rows, 16 per load, over 4 waves (the vmcnt(6) of the main loop)");
+static_assert(NSTAGE == 3, "the vmcnt waits of the main loop are written for a 3-deep ring");
+static_assert(THREADS == TC && TR <= THREADS, "the prologue and the final merge map thread t to column t");
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef int int4v __attribute__((ext_vector_type(4)));
+constexpr int kBufferFlags = 0x00020000;     // buffer resource word 3 for raw byte-addressed loads
 
 // ---------------------------------------------------------------------------
 // Prepare: one wave per row.  norms[] exactly as msm_norms_kernel; inv[] holds the
@@ -76,53 +87,57 @@ __global__ __launch_bounds__(256) void split_prepare_kernel(const float* __restr
     }
   }
   const double sc = acc > 0.0 ? ldexp(1.0 / sqrt(acc), kScaleShift) : 0.0;
-  _Float16* dst = hl + row * (long long)nkb * 64;
+  _Float16* dst = hl + row * (long long)nkb * (2 * KB);
   const int cp = nkb * KB;
   for (int k = lane; k < cp; k += kWave) {
     const double v = k < c ? (double)src[k] * sc : 0.0;
     const _Float16 hi = (_Float16)(float)v;
     const _Float16 lo = (_Float16)(float)(v - (double)(float)hi);
-    dst[(k / KB) * 64 + (k % KB)] = hi;
-    dst[(k / KB) * 64 + KB + (k % KB)] = lo;
+    dst[(k / KB) * (2 * KB) + (k % KB)] = hi;
+    dst[(k / KB) * (2 * KB) + KB + (k % KB)] = lo;
   }
 }
 
 // ---------------------------------------------------------------------------
-// Pair minima.
+// Pair minima.  Workgroup w takes half (w & 1) -- 128 rows x all 256 columns -- of
+// triangle tile (w >> 1); two workgroups share a CU, so one's barrier and LDS-read
+// bubbles are covered by the other's MFMAs.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* __restrict__ hl,
+__global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* __restrict__ hl,
                                                                const float* __restrict__ norms,
                                                                const float* __restrict__ inv,
                                                                uint32_t* __restrict__ minbits, int rows, int n, int p,
                                                                int nkb, int T, long long ntiles) {
-  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * kStageBytes];
-  __shared__ __attribute__((aligned(16))) float s_rnorm[TM];
-  __shared__ __attribute__((aligned(16))) float s_cnorm[TM];
-  __shared__ __attribute__((aligned(16))) float s_rinv[TM];
-  __shared__ __attribute__((aligned(16))) float s_cinv[TM];
-  __shared__ __attribute__((aligned(16))) int s_rimg[TM];
-  __shared__ int s_cimg[TM];
+  __shared__ __attribute__((aligned(16))) unsigned char smem[NSTAGE * kStageBytes];
+  __shared__ __attribute__((aligned(16))) float s_rnorm[TR];
+  __shared__ __attribute__((aligned(16))) float s_rinv[TR];
+  __shared__ __attribute__((aligned(16))) int s_rimg[TR];
+  __shared__ float s_cnorm[TC];
+  __shared__ float s_cinv[TC];
+  __shared__ int s_cimg[TC];
 
   const long long w = xcd_logical_id(blockIdx.x, gridDim.x);
-  if (w >= ntiles) return;
-  const int2 tile = decode_tile(w, T);
-  const int row0 = tile.x * TM, col0 = tile.y * TM;
-  const int rlast = min(row0 + TM, rows) - 1, clast = min(col0 + TM, rows) - 1;
+  if (w >= 2 * ntiles) return;
+  const int2 tile = decode_tile(w >> 1, T);
+  const int row0 = tile.x * TM + (int)(w & 1) * TR, col0 = tile.y * TM;
+  if (row0 >= rows) return;  // lower half of a last tile row that lies in padding
+  const int rlast = min(row0 + TR, rows) - 1, clast = min(col0 + TC, rows) - 1;
   const int rimg0 = row0 / p, cimg0 = col0 / p;
-  const bool simple = (row0 + TM <= rows) && (col0 + TM <= rows) && (rlast / p == rimg0) && (clast / p == cimg0);
+  const bool simple = (row0 + TR <= rows) && (col0 + TC <= rows) && (rlast / p == rimg0) && (clast / p == cimg0);
   if (simple && rimg0 == cimg0) return;
 
-  const int t = threadIdx.x;
-  if (t < TM) {
-    const int r = row0 + t;
-    s_rnorm[t] = r < rows ? norms[r] : 0.f;
-    s_rinv[t] = r < rows ? inv[r] : 0.f;
-    s_rimg[t] = r < rows ? r / p : n;  // n marks "no image" (padding)
-  } else {
-    const int j = t - TM, cc = col0 + j;
-    s_cnorm[j] = cc < rows ? norms[cc] : 0.f;
-    s_cinv[j] = cc < rows ? inv[cc] : 0.f;
-    s_cimg[j] = cc < rows ? cc / p : n;
+  const int t = threadIdx.x;  // THREADS == TC: thread t stages column t and, for t < TR, row t
+  {
+    const int cc = col0 + t;
+    s_cnorm[t] = cc < rows ? norms[cc] : 0.f;
+    s_cinv[t] = cc < rows ? inv[cc] : 0.f;
+    s_cimg[t] = cc < rows ? cc / p : n;  // n marks "no image" (padding)
+    if (t < TR) {
+      const int r = row0 + t;
+      s_rnorm[t] = r < rows ? norms[r] : 0.f;
+      s_rinv[t] = r < rows ? inv[r] : 0.f;
+      s_rimg[t] = r < rows ? r / p : n;
+    }
   }
 
   const int wave = t / kWave, lane = t % kWave;
@@ -137,68 +152,102 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.f;
 
-  // Loads: wave wv fills staged rows wv*64 .. wv*64 + 63, eight per load; staged rows
-  // 0..255 are tile rows (A), 256..511 tile columns (B).  Lane l of a load carries
-  // row R = R0 + l/8, LDS position l % 8, i.e. segment (l % 8) ^ (R & 7) = (l % 8) ^
-  // (l / 8).  Padded rows re-read the last row (masked in the epilogue).
-  const int lrow8 = lane >> 3, lseg = (lane & 7) ^ lrow8;
+  // Loads go straight from global memory into LDS (buffer_load_dwordx4 ... lds: lane
+  // l of a load lands at M0 + 16 l, so one load fills 16 staged rows of 64 bytes).
+  // Wave wv fills staged rows wv*96 .. wv*96 + 95; staged rows 0..127 are tile rows
+  // (A), 128..383 tile columns (B).  Lane l of a load carries row R = R0 + l/4 into
+  // LDS position l % 4, i.e. segment (l % 4) ^ ((R >> 2) & 3).  Padded rows re-read
+  // the last row (masked in the epilogue).
+  // Addressing: a buffer resource over the split array, one 32-bit byte offset per
+  // load (row base + segment, loop-invariant) and the stage offset as the scalar
+  // offset; offsets past the array read zeros.  The loads are issued from inline
+  // assembly so that the compiler, which cannot tell the ring buffers apart, does
+  // not wait for them before reading another buffer; the loop waits for them
+  // explicitly.
+  const int lrow = lane >> 2;
+  const unsigned long long hl_addr = reinterpret_cast<unsigned long long>(hl);
+  int4v rsrc;
+  rsrc.x = (int)(uint32_t)(hl_addr & 0xffffffffull);
+  rsrc.y = (int)(uint32_t)(hl_addr >> 32);  // base high bits; stride 0
+  rsrc.z = (int)(uint32_t)((long long)rows * nkb * ROWB);
+  rsrc.w = kBufferFlags;
+  constexpr int kWaveRows = kStageRows / (THREADS / kWave);
+  uint32_t voff[kLoads];
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    const int R = wave * kWaveRows + i * kRowsPerLoad + lrow;
+    const int grow = R < TR ? min(row0 + R, rows - 1) : min(col0 + R - TR, rows - 1);
+    const int lseg = (lane & 3) ^ ((R >> 2) & 3);
+    voff[i] = (uint32_t)grow * (uint32_t)(nkb * ROWB) + (uint32_t)(lseg * 16);
+  }
+  const uint32_t lds0 = (uint32_t)(size_t)(lds_void*)smem;
   auto issue = [&](int kb, int buf) {
+    const uint32_t soff = (uint32_t)(kb * ROWB);
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
-      const int R0 = wave * 64 + i * 8;
-      const int R = R0 + lrow8;
-      const int grow = R < TM ? min(row0 + R, rows - 1) : min(col0 + R - TM, rows - 1);
-      __builtin_amdgcn_global_load_lds(hl + ((long long)grow * nkb + kb) * 64 + lseg * 8,
-                                       (lds_void*)(smem + buf * kStageBytes + R0 * ROWB), 16, 0, 0);
+      // wave-uniform LDS base of this load (M0 is a scalar register)
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+          lds0 + (uint32_t)(buf * kStageBytes + (wave * kWaveRows + i * kRowsPerLoad) * ROWB));
+      // s_nop: one wait state between the scalar write of M0 and the load that reads it
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                   :
+                   : "s"(m0), "v"(voff[i]), "s"(rsrc), "s"(soff)
+                   : "memory", "m0");
     }
   };
-  // operand of staged row r, segment sg (hi: 0..3, lo: 4..7); r & 7 == lr & 7 here
-  const int sw = lr & 7;
+  // Segments of a staged row: 0, 1 = hi channels 0-7, 8-15; 2, 3 = lo.  Segment s of
+  // staged row r sits at position s ^ ((r >> 2) & 3); the operand rows here are
+  // (multiple of 32) + lr, so the swizzle is (lr >> 2) & 3.  Over any 16 consecutive
+  // rows (the lanes an LDS read serves together) the pairs (r & 3, (r >> 2) & 3) take
+  // 16 distinct 16-byte slots of a 256-byte bank window: conflict-free reads.
+  const int sw = (lr >> 2) & 3;
+  const int phi = (lh ^ sw) * 16, plo = ((2 + lh) ^ sw) * 16;
   auto compute = [&](int buf) {
     const unsigned char* As = smem + buf * kStageBytes + (wm * 64 + lr) * ROWB;
-    const unsigned char* Bs = smem + buf * kStageBytes + (TM + wn * 128 + lr) * ROWB;
+    const unsigned char* Bs = smem + buf * kStageBytes + (TR + wn * 128 + lr) * ROWB;
+    half8 ahi[2], alo[2], bhi[4], blo[4];
 #pragma unroll
-    for (int j = 0; j < KB / 16; ++j) {
-      const int phi = ((2 * j + lh) ^ sw) * 16, plo = ((4 + 2 * j + lh) ^ sw) * 16;
-      half8 ahi[2], alo[2], bhi[4], blo[4];
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        ahi[mb] = *reinterpret_cast<const half8*>(As + mb * 32 * ROWB + phi);
-        alo[mb] = *reinterpret_cast<const half8*>(As + mb * 32 * ROWB + plo);
-      }
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        bhi[nb] = *reinterpret_cast<const half8*>(Bs + nb * 32 * ROWB + phi);
-        blo[nb] = *reinterpret_cast<const half8*>(Bs + nb * 32 * ROWB + plo);
-      }
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
-          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[mb], bhi[nb], acc[mb][nb], 0, 0, 0);
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
-          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[mb], blo[nb], acc[mb][nb], 0, 0, 0);
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
-          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo[mb], bhi[nb], acc[mb][nb], 0, 0, 0);
+    for (int mb = 0; mb < 2; ++mb) {
+      ahi[mb] = *reinterpret_cast<const half8*>(As + mb * 32 * ROWB + phi);
+      alo[mb] = *reinterpret_cast<const half8*>(As + mb * 32 * ROWB + plo);
     }
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      bhi[nb] = *reinterpret_cast<const half8*>(Bs + nb * 32 * ROWB + phi);
+      blo[nb] = *reinterpret_cast<const half8*>(Bs + nb * 32 * ROWB + plo);
+    }
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[mb], bhi[nb], acc[mb][nb], 0, 0, 0);
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[mb], blo[nb], acc[mb][nb], 0, 0, 0);
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo[mb], bhi[nb], acc[mb][nb], 0, 0, 0);
   };
 
-  // Stage kc lives in LDS buffer kc & 1.  Iteration kc waits for its own loads of
-  // stage kc, then the barrier makes every wave's loads visible and guarantees that
-  // buffer (kc + 1) & 1 is no longer read (compute(kc - 1) is done everywhere), so
-  // the loads of stage kc + 1 go out before compute(kc) and have its duration to land.
-  issue(0, 0);
+  // Stage kc lives in LDS buffer kc % NSTAGE and its loads go out NSTAGE - 1 stages
+  // ahead.  Iteration kc waits until this thread's loads of stage kc have landed
+  // (loads complete in order, so only the next stage's kLoads may still be in
+  // flight); the barrier then makes every wave's loads visible and guarantees that
+  // buffer (kc - 1) % NSTAGE is no longer read (compute(kc - 1) is done everywhere),
+  // so the loads of stage kc + NSTAGE - 1 can refill it.
+  for (int st = 0; st < NSTAGE - 1 && st < nkb; ++st) issue(st, st);
   for (int kc = 0; kc < nkb; ++kc) {
-    __builtin_amdgcn_s_waitcnt(0);
+    if (kc + 1 < nkb)
+      asm volatile("s_waitcnt vmcnt(6)" ::: "memory");  // the next stage's kLoads may be in flight
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (kc + 1 < nkb) issue(kc + 1, (kc + 1) & 1);
-    compute(kc & 1);
+    if (kc + NSTAGE - 1 < nkb) issue(kc + NSTAGE - 1, (kc + NSTAGE - 1) % NSTAGE);
+    compute(kc % NSTAGE);
   }
 
   // Epilogue.  Lane (lr, lh) of wave (wm, wn) holds, for mb < 2, nb < 4, v < 16, the
@@ -266,20 +315,15 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
         rv[mb * 16 + v] = fminf(fminf(d2[mb][0][v], d2[mb][1][v]), fminf(d2[mb][2][v], d2[mb][3][v]));
     transpose_min32(rv, lr);
     __syncthreads();  // operand buffers are no longer read
-    float* s_cmin = reinterpret_cast<float*>(smem);  // [4 (wm)][TM]
-    float* s_rmin = s_cmin + 4 * TM;                  // [2 (wn)][TM]
+    float* s_cmin = reinterpret_cast<float*>(smem);  // [2 (wm)][TC]
+    float* s_rmin = s_cmin + 2 * TC;                  // [2 (wn)][TR]
 #pragma unroll
-    for (int q = 0; q < 2; ++q) s_cmin[wm * TM + wn * 128 + (2 * q + lh) * 32 + lr] = cm[q];
-    s_rmin[wn * TM + wm * 64 + transposed_row(lr, lh)] = rv[0];
+    for (int q = 0; q < 2; ++q) s_cmin[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = cm[q];
+    s_rmin[wn * TR + wm * 64 + transposed_row(lr, lh)] = rv[0];
     __syncthreads();
-    if (t < TM) {
-      const float m = fminf(s_rmin[t], s_rmin[TM + t]);
-      atomicMin(minbits + (long long)(row0 + t) * n + cA, __float_as_uint(m));
-    } else {
-      const int j = t - TM;
-      const float m = fminf(fminf(s_cmin[j], s_cmin[TM + j]), fminf(s_cmin[2 * TM + j], s_cmin[3 * TM + j]));
-      atomicMin(minbits + (long long)(col0 + j) * n + rA, __float_as_uint(m));
-    }
+    atomicMin(minbits + (long long)(col0 + t) * n + rA, __float_as_uint(fminf(s_cmin[t], s_cmin[TC + t])));
+    if (t < TR)
+      atomicMin(minbits + (long long)(row0 + t) * n + cA, __float_as_uint(fminf(s_rmin[t], s_rmin[TR + t])));
     return;
   }
 
@@ -339,42 +383,42 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
     rowminB = transpose_min32(rv, lr);
   }
   __syncthreads();  // operand buffers are no longer read
-  float* s_cminA = reinterpret_cast<float*>(smem);  // [4 (wm)][TM]
-  float* s_cminB = s_cminA + 4 * TM;
-  float* s_rminA = s_cminB + 4 * TM;                 // [2 (wn)][TM]
-  float* s_rminB = s_rminA + 2 * TM;
+  float* s_cminA = reinterpret_cast<float*>(smem);  // [2 (wm)][TC]
+  float* s_cminB = s_cminA + 2 * TC;
+  float* s_rminA = s_cminB + 2 * TC;                 // [2 (wn)][TR]
+  float* s_rminB = s_rminA + 2 * TR;
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    s_cminA[wm * TM + wn * 128 + (2 * q + lh) * 32 + lr] = cmA[q];
-    s_cminB[wm * TM + wn * 128 + (2 * q + lh) * 32 + lr] = cmB[q];
+    s_cminA[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = cmA[q];
+    s_cminB[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = cmB[q];
   }
   const int rk = wm * 64 + transposed_row(lr, lh);
-  s_rminA[wn * TM + rk] = rowminA;
-  s_rminB[wn * TM + rk] = rowminB;
+  s_rminA[wn * TR + rk] = rowminA;
+  s_rminB[wn * TR + rk] = rowminB;
   __syncthreads();
-  if (t < TM) {
-    const int r = row0 + t;
-    if (r < rows) {
-      const float a = fminf(s_rminA[t], s_rminA[TM + t]);
-      const float b = fminf(s_rminB[t], s_rminB[TM + t]);
-      if (a < inf) atomicMin(minbits + (long long)r * n + cA, __float_as_uint(a));
-      if (b < inf) atomicMin(minbits + (long long)r * n + cA + 1, __float_as_uint(b));
-    }
-  } else {
-    const int j = t - TM;
-    const int cc = col0 + j;
+  {
+    const int cc = col0 + t;
     if (cc < rows) {
-      const float a = fminf(fminf(s_cminA[j], s_cminA[TM + j]), fminf(s_cminA[2 * TM + j], s_cminA[3 * TM + j]));
-      const float b = fminf(fminf(s_cminB[j], s_cminB[TM + j]), fminf(s_cminB[2 * TM + j], s_cminB[3 * TM + j]));
+      const float a = fminf(s_cminA[t], s_cminA[TC + t]);
+      const float b = fminf(s_cminB[t], s_cminB[TC + t]);
       if (a < inf) atomicMin(minbits + (long long)cc * n + rA, __float_as_uint(a));
       if (b < inf) atomicMin(minbits + (long long)cc * n + rA + 1, __float_as_uint(b));
+    }
+  }
+  if (t < TR) {
+    const int r = row0 + t;
+    if (r < rows) {
+      const float a = fminf(s_rminA[t], s_rminA[TR + t]);
+      const float b = fminf(s_rminB[t], s_rminB[TR + t]);
+      if (a < inf) atomicMin(minbits + (long long)r * n + cA, __float_as_uint(a));
+      if (b < inf) atomicMin(minbits + (long long)r * n + cA + 1, __float_as_uint(b));
     }
   }
 }
 
 inline int nkb_of(int c) { return (c + KB - 1) / KB; }
 
-inline size_t split_array_bytes(long long rows, int c) { return align_up((size_t)rows * nkb_of(c) * 64 * 2, 256); }
+inline size_t split_array_bytes(long long rows, int c) { return align_up((size_t)rows * nkb_of(c) * ROWB, 256); }
 
 inline size_t workspace_bytes(long long n, long long p, int c) {
   return msm::workspace_bytes(n, p) + split_array_bytes(n * p, c);
@@ -388,6 +432,7 @@ inline int validate(int n, int p, int c, void* ws, size_t ws_bytes) {
   if (n < 2 || p < 1 || c < 1) return MUSC_ERR_INVALID_ARG;
   const long long rows = (long long)n * p;
   if (rows > (1LL << 30) || n > 4096) return MUSC_ERR_UNSUPPORTED;
+  if (rows * nkb_of(c) * (long long)ROWB > 0xffffffffLL) return MUSC_ERR_UNSUPPORTED;  // 32-bit buffer offsets
   if (!ws || ws_bytes < workspace_bytes(n, p, c)) return MUSC_ERR_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0) return MUSC_ERR_INVALID_ARG;
   return MUSC_OK;
@@ -406,7 +451,7 @@ inline int run_pairs(int n, int p, int c, void* ws, hipStream_t s) {
   const long long rows = (long long)n * p;
   const long long T = (rows + TM - 1) / TM;
   const long long ntiles = total_tiles(T);
-  const long long grid = (ntiles + kXcds - 1) / kXcds * kXcds;
+  const long long grid = (2 * ntiles + kXcds - 1) / kXcds * kXcds;  // two half-tile workgroups per tile
   if (grid > 0x7fffffffLL) return MUSC_ERR_UNSUPPORTED;
   const Workspace w = carve(ws, n, p);
   hipLaunchKernelGGL(split_pair_kernel, dim3((unsigned)grid), dim3(THREADS), 0, s, split_array(ws, n, p), w.norms,

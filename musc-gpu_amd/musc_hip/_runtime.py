@@ -70,6 +70,7 @@ SIGNATURES = {
     'musc_calibrate_hbm_stream': (_i, [_i, _vp, _vp, _ll, _vp]),
     'musc_calibrate_lnamd_pattern': (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     'musc_calibrate_mfma_f32': (_i, [_vp, _i, _i, ctypes.POINTER(ctypes.c_double), _vp]),
+    'musc_calibrate_mfma_f16': (_i, [_vp, _i, _i, ctypes.POINTER(ctypes.c_double), _vp]),
 }
 
 _lock = threading.Lock()

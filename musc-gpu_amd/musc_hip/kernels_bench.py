@@ -254,25 +254,28 @@ def bench_e2e(args):
 
 
 def bench_mfma_peak(args):
-    """Sustained fp32 MFMA rate with no memory traffic (musc_calibrate_mfma_f32)."""
+    """Sustained fp32 and fp16 MFMA rates with no memory traffic (musc_calibrate_mfma_f32 / _f16)."""
     import ctypes
     dev = torch.device('cuda:0')
     blocks = 256 * 8
     out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
-    flop = ctypes.c_double()
-    ts = []
-    for it in range(args.iters + 1):
-        e0, e1 = _events()
-        e0.record()
-        rt.check(rt.library().musc_calibrate_mfma_f32(out.data_ptr(), blocks, 2000, ctypes.byref(flop),
-                                                      rt.stream(dev)), 'musc_calibrate_mfma_f32')
-        e1.record()
-        torch.cuda.synchronize()
-        if it > 0:
-            ts.append(e0.elapsed_time(e1))
-    ms = sum(ts) / len(ts)
-    tf = flop.value / (ms / 1e3) / 1e12
-    return {'kernel': 'mfma_peak', 'avg_ms': ms, 'tflops': tf, 'frac_datasheet_peak': tf / FP32_MFMA_TFLOPS}
+    res = {'kernel': 'mfma_peak'}
+    for name, fn, peak in (('fp32', 'musc_calibrate_mfma_f32', FP32_MFMA_TFLOPS),
+                           ('fp16', 'musc_calibrate_mfma_f16', FP16_MFMA_TFLOPS)):
+        flop = ctypes.c_double()
+        ts = []
+        for it in range(args.iters + 1):
+            e0, e1 = _events()
+            e0.record()
+            rt.check(getattr(rt.library(), fn)(out.data_ptr(), blocks, 2000, ctypes.byref(flop), rt.stream(dev)), fn)
+            e1.record()
+            torch.cuda.synchronize()
+            if it > 0:
+                ts.append(e0.elapsed_time(e1))
+        ms = sum(ts) / len(ts)
+        tf = flop.value / (ms / 1e3) / 1e12
+        res[name] = {'avg_ms': ms, 'tflops': tf, 'frac_datasheet_peak': tf / peak}
+    return res
 
 
 def bench_copy(args):
