@@ -18,6 +18,11 @@ average duration from torch.cuda (HIP) events recorded around every launch in
 the timed region on the stream it runs on.  The CPU baseline is the oracle's
 restatement of the reference's original torch backend, timed on a bounded
 sample on this host and extrapolated to the whole job.
+
+The same step is then timed with the split MSM engine (each fp32 dot product
+formed from three fp16 MFMA products, musc_msm_split_*), reported in
+`split16_engine` with its own fp16-MFMA roofline and its agreement with the
+fp32 engine's maps; `--no-split` skips it.  The headline stays the fp32 engine.
 """
 from __future__ import annotations
 
@@ -33,6 +38,7 @@ for _p in (ROOT, os.path.join(ROOT, 'musc-gpu_amd')):
         sys.path.insert(0, _p)
 
 FP32_MFMA_PEAK_TFLOPS = 157.3
+FP16_MFMA_PEAK_TFLOPS = 2500.0
 HBM_PEAK_GBPS = 8000.0
 
 CONFIGS = {
@@ -129,6 +135,8 @@ def main() -> int:
     ap.add_argument('--config', choices=sorted(CONFIGS), default='pool')
     ap.add_argument('--seed', type=int, default=42)
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--no-split', action='store_true',
+                    help='skip the second measurement with the split (3x fp16 MFMA) MSM engine')
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU only: this build has no multi-GPU path (--gpus {args.gpus} requested). '
@@ -136,7 +144,7 @@ def main() -> int:
         return 2
 
     import torch
-    from musc_hip import pipeline, synthetic
+    from musc_hip import _MSM_hip, pipeline, synthetic
     from musc_hip import _runtime as rt
 
     if not torch.cuda.is_available():
@@ -228,6 +236,35 @@ def main() -> int:
                                         'note': 'stats + finalize + stream kernels timed together'}},
         'cpu_baseline': None,
     }
+    if not args.no_split and p >= _MSM_hip.SPLIT_MIN_P:
+        # The same step with the split MSM engine (fp32 dot products from three fp16 MFMA
+        # products), reported beside the headline; its maps are compared with the fp32
+        # engine's maps of the timed run above.
+        for w in range(args.warmup):
+            pipeline.score_pool(tokens, r_list, image_size, msm_engine='split16')
+        torch.cuda.synchronize()
+        sp_timing: dict = {}
+        t2 = time.perf_counter()
+        for s_ in range(args.steps):
+            maps16, img16 = pipeline.score_pool(tokens, r_list, image_size, timing=sp_timing, msm_engine='split16')
+        torch.cuda.synchronize()
+        sp_elapsed = time.perf_counter() - t2
+        sp_pair_ms = [a.elapsed_time(b) for a, b in sp_timing['pairs']]
+        sp_pair_s = sum(sp_pair_ms) / len(sp_pair_ms) / 1e3
+        sp_tf = flop_per_launch / sp_pair_s / 1e12
+        result['split16_engine'] = {
+            'value': n * args.steps / sp_elapsed, 'unit': 'images/s', 'ms_per_step': sp_elapsed / args.steps * 1e3,
+            'dtype': 'fp16 MFMA products (hi.hi + hi.lo + lo.hi), fp32 accumulation',
+            'pair_kernel': 'split_pair_kernel', 'avg_launch_ms': sp_pair_s * 1e3, 'launches': len(sp_pair_ms),
+            'fp32_equivalent_tflops': sp_tf,
+            'roofline': {'bound': 'mfma', 'achieved': 3 * sp_tf, 'peak': FP16_MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
+                         'frac': 3 * sp_tf / FP16_MFMA_PEAK_TFLOPS,
+                         'note': 'three fp16 MFMA products per algorithmic fp32 dot product'},
+            'max_abs_diff_maps_vs_fp32_engine': (maps16 - maps).abs().max().item(),
+            'max_abs_diff_image_scores_vs_fp32_engine': (img16 - img).abs().max().item(),
+        }
+        log(f'[bench] split16 engine: {args.steps} steps in {sp_elapsed:.3f} s')
+        del maps16, img16
     if not args.no_cpu_baseline:
         log('[bench] timing the CPU baseline (oracle restatement, bounded sample)')
         pools = pipeline.lnamd_pools(tokens, r_list)
