@@ -52,6 +52,27 @@ def test_msm_workspace_bytes(lib):
     assert lib.musc_msm_workspace_bytes(1, 10, 10, ctypes.byref(out)) == 1001
 
 
+def test_msm_split_workspace_and_argument_errors(lib):
+    align = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    out, base = ctypes.c_size_t(), ctypes.c_size_t()
+    assert lib.musc_msm_split_workspace_bytes(83, 1369, 1024, ctypes.byref(out)) == 0
+    assert lib.musc_msm_workspace_bytes(83, 1369, 1024, ctypes.byref(base)) == 0
+    # the fp32 engine's workspace, then hi[16] | lo[16] fp16 (64 bytes) per row and 16-channel block
+    assert out.value == base.value + align(83 * 1369 * (1024 // 16) * 64)
+    assert lib.musc_msm_split_workspace_bytes(5, 300, 33, ctypes.byref(out)) == 0
+    assert lib.musc_msm_workspace_bytes(5, 300, 33, ctypes.byref(base)) == 0
+    assert out.value == base.value + align(5 * 300 * 3 * 64)  # 33 channels -> 3 zero-padded blocks
+    assert lib.musc_msm_split_workspace_bytes(1, 300, 16, ctypes.byref(out)) == 1001
+    fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    big = ctypes.c_size_t(1 << 40)
+    assert lib.musc_msm_split_scores_f32(fake, 8, 300, 16, 2, 2, 0, fake, fake, big, None) == 1001  # empty window
+    assert lib.musc_msm_split_scores_f32(fake, 8, 300, 16, 0, 2, 4, fake, fake, big, None) == 1001  # unknown flag
+    assert lib.musc_msm_split_scores_f32(fake, 8, 100, 16, 0, 2, 0, fake, fake, big, None) == 1003  # p < 256
+    assert lib.musc_msm_split_scores_f32(fake, 8, 300, 16, 0, 2, 0, fake, fake, ctypes.c_size_t(16), None) == 1002
+    assert lib.musc_msm_split_prepare_f32(None, 8, 300, 16, 0, fake, big, None) == 1001
+    assert lib.musc_msm_split_pair_minima(8, 300, 16, fake, ctypes.c_size_t(16), None) == 1002
+
+
 def test_msm_argument_errors_before_any_launch(lib):
     fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
     big = ctypes.c_size_t(1 << 40)
