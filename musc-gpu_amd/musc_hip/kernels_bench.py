@@ -6,6 +6,7 @@
     python musc-gpu_amd/musc_hip/kernels_bench.py copy [--mib 1024 --iters 3]
     python musc-gpu_amd/musc_hip/kernels_bench.py super_fast [--n 83 --iters 3] (config 3 from tokens)
     python musc-gpu_amd/musc_hip/kernels_bench.py e2e --n 160 --iters 1       (config 5)
+    (msm, super_fast and e2e take --engine fp32|split16 for the MSM dot products)
     python musc-gpu_amd/musc_hip/kernels_bench.py mfma_peak                   (device calibration)
     python musc-gpu_amd/musc_hip/kernels_bench.py hbm                         (HBM calibration)
     python musc-gpu_amd/musc_hip/kernels_bench.py msm lnamd copy --iters 1   (several in one process)
@@ -128,7 +129,7 @@ def bench_super_fast(args):
         timing = {}
         e0, e1 = _events()
         e0.record()
-        pipeline.score_pool(toks, r_list=[3], image_size=518, pool_grid=28, timing=timing)
+        pipeline.score_pool(toks, r_list=[3], image_size=518, pool_grid=28, timing=timing, msm_engine=args.engine)
         e1.record()
         torch.cuda.synchronize()
         if it > 0:
@@ -142,7 +143,7 @@ def bench_super_fast(args):
     p = 784
     flop = 1024.0 * p * p * n * (n - 1)
     nbytes = 4.0 * n * (1370 * 1024 + p * 1024)     # tokens read once, pooled pool written once
-    return {'kernel': 'super_fast', 'n': n, 'total_ms': total, 'images_per_s': n / (total / 1e3),
+    return {'kernel': 'super_fast', 'engine': args.engine, 'n': n, 'total_ms': total, 'images_per_s': n / (total / 1e3),
             'lnamd_pooled_ms': lnamd, 'lnamd_pooled_gbps': nbytes / (lnamd / 1e3) / 1e9, 'pair_ms': pair,
             'pair_tflops': flop / (pair / 1e3) / 1e12}
 
@@ -241,7 +242,7 @@ def bench_e2e(args):
     ts = []
     for it in range(args.iters + 1):
         timing = {}
-        out = pipeline.run_category(model, imgs, timing=timing)
+        out = pipeline.run_category(model, imgs, timing=timing, msm_engine=args.engine)
         torch.cuda.synchronize()
         e0, e1, e2, e3 = timing['events'][0]
         if it > 0:
@@ -249,7 +250,7 @@ def bench_e2e(args):
         print(f'[e2e] iteration {it} done', file=sys.stderr, flush=True)
         del out
     enc, score, rsc, total = (sum(t[i] for t in ts) / len(ts) for i in range(4))
-    return {'kernel': 'e2e', 'n': args.n, 'encoder_ms': enc, 'lnamd_msm_epilogue_ms': score, 'rscin_ms': rsc,
+    return {'kernel': 'e2e', 'engine': args.engine, 'n': args.n, 'encoder_ms': enc, 'lnamd_msm_epilogue_ms': score, 'rscin_ms': rsc,
             'total_ms': total, 'images_per_s': args.n / (total / 1e3), 'anomalous_images': anomalous}
 
 

@@ -118,14 +118,15 @@ def score_pool(tokens: list[torch.Tensor], r_list=(1, 3, 5), image_size: int = 5
 
 def run_category(model, images: torch.Tensor, feature_layers=(5, 11, 17, 23), r_list=(1, 3, 5),
                  batch_size: int = 4, image_size: int | None = None, k_list=(1, 2, 3), autocast: bool = True,
-                 pool_grid: int | None = None, timing: dict | None = None):
+                 pool_grid: int | None = None, timing: dict | None = None, msm_engine: str = 'fp32'):
     """One division of MuSc.make_category_data's hot path (models/musc.py:163-296) on the GPU.
 
     images (N, 3, S, S) normalised GPU tensor -> dict with 'maps' (N, 1, S, S) float64,
     'image_scores' (N,) float64 map maxima, 'scores' (N,) fp32 after RsCIN, 'class_tokens'
     (N, D) fp32.  The encoder runs in batches of `batch_size` under fp16 autocast (as at
     musc.py:196) with the fused attention (musc_hip._encoder_hip); layer tokens stay on
-    the GPU; then LNAMD, MSM, the epilogue and RsCIN run as in score_pool.
+    the GPU; then LNAMD, MSM (engine `msm_engine`), the epilogue and RsCIN run as in
+    score_pool.
     """
     from . import _encoder_hip
 
@@ -149,7 +150,8 @@ def run_category(model, images: torch.Tensor, feature_layers=(5, 11, 17, 23), r_
     class_tokens = torch.cat(cls, 0)
     if timing is not None:
         e1 = ev(); e1.record()
-    maps, image_scores = score_pool(tokens, r_list=r_list, image_size=image_size, pool_grid=pool_grid)
+    maps, image_scores = score_pool(tokens, r_list=r_list, image_size=image_size, pool_grid=pool_grid,
+                                    msm_engine=msm_engine)
     if timing is not None:
         e2 = ev(); e2.record()
     scores = RsCIN(image_scores, class_tokens, list(k_list))
