@@ -22,24 +22,26 @@ constexpr uint32_t kInfBits = 0x7f800000u;
 // then the rectangle in column-major order, so that the workgroups one XCD runs
 // at the same time share a few A and B panels.
 // ---------------------------------------------------------------------------
+template <int kBand = BAND>
 __host__ __device__ inline long long band_prefix(long long s, long long T) {
-  // tiles in bands 0..s-1, all of which are full (BAND rows)
-  return 36LL * s + 8LL * (T - 8) * s - 32LL * s * (s - 1);
+  // tiles in bands 0..s-1, all of which are full (kBand rows; row i holds T - i tiles)
+  return s * kBand * T - (long long)kBand * kBand * s * (s - 1) / 2 - s * (long long)kBand * (kBand - 1) / 2;
 }
 
 __host__ __device__ inline long long total_tiles(long long T) { return T * (T + 1) / 2; }
 
+template <int kBand = BAND>
 __device__ inline int2 decode_tile(long long w, long long T) {
-  const long long nb = (T + BAND - 1) / BAND;
+  const long long nb = (T + kBand - 1) / kBand;
   long long lo = 0, hi = nb - 1;  // largest s with band_prefix(s) <= w
   while (lo < hi) {
     long long mid = (lo + hi + 1) >> 1;
-    if (band_prefix(mid, T) <= w) lo = mid; else hi = mid - 1;
+    if (band_prefix<kBand>(mid, T) <= w) lo = mid; else hi = mid - 1;
   }
   const long long s = lo;
-  const long long I0 = s * BAND;
-  const long long h = (T - I0) < BAND ? (T - I0) : BAND;
-  long long q = w - band_prefix(s, T);
+  const long long I0 = s * kBand;
+  const long long h = (T - I0) < kBand ? (T - I0) : kBand;
+  long long q = w - band_prefix<kBand>(s, T);
   const long long tri = h * (h + 1) / 2;
   if (q < tri) {
     long long jl = (long long)((sqrt(8.0 * (double)q + 1.0) - 1.0) * 0.5);

@@ -52,6 +52,7 @@ constexpr int THREADS = 256;                 // 4 waves: 2 (rows) x 2 (columns) 
 constexpr int kStageRows = TR + TC;          // A rows then B rows
 constexpr int kStageBytes = kStageRows * ROWB;  // 24 KB
 constexpr int kScaleShift = 10;              // normalised rows are scaled by 2^10
+constexpr int kBandSplit = BAND;             // tile rows per band of the triangle enumeration
 constexpr int kRowsPerLoad = kWave * 16 / ROWB;                          // 16 staged rows per direct load
 constexpr int kLoads = kStageRows / kRowsPerLoad / (THREADS / kWave);    // direct loads per wave per stage
 
@@ -118,7 +119,7 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
 
   const long long w = xcd_logical_id(blockIdx.x, gridDim.x);
   if (w >= 2 * ntiles) return;
-  const int2 tile = decode_tile(w >> 1, T);
+  const int2 tile = decode_tile<kBandSplit>(w >> 1, T);
   const int row0 = tile.x * TM + (int)(w & 1) * TR, col0 = tile.y * TM;
   if (row0 >= rows) return;  // lower half of a last tile row that lies in padding
   const int rlast = min(row0 + TR, rows) - 1, clast = min(col0 + TC, rows) - 1;
