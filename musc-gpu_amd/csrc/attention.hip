@@ -28,6 +28,12 @@ constexpr int KB = 32;              // keys per block
 constexpr int QW = 32;              // queries per wave
 constexpr int WAVES = 4;
 constexpr int KPITCH = D + 4;       // K block row pitch (floats)
+
+// 2^x for the online softmax: the bare v_exp_f32 (about 1 ulp).  exp2f adds a
+// rescaling path for results below 2^-126; the arguments here are <= 0 and such
+// terms are far below what the fp32 sums and fp16 probabilities resolve, so that
+// path (5 VALU instructions per exponential) is dropped.
+__device__ inline float softmax_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 constexpr int VPITCH = KB + 4;      // V^T block row pitch (floats)
 
 // Where head bh = b * heads + h of a (batch, heads, t, 64) tensor lives: element
@@ -167,12 +173,12 @@ __global__ __launch_bounds__(WAVES * kWave, 3) void attn_fwd_kernel(const float*
     float psum = 0.f;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      s[v] = exp2f(s[v] - mnew);
+      s[v] = softmax_exp2(s[v] - mnew);
       psum += s[v];
     }
     psum += __shfl_xor(psum, 32, kWave);
     if (!__all(mnew == m)) {  // rescale only when some running maximum moved
-      const float alpha = exp2f(m - mnew);  // 0 on the first block (m = -inf)
+      const float alpha = softmax_exp2(m - mnew);  // 0 on the first block (m = -inf)
       l *= alpha;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
@@ -320,13 +326,13 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
     half8 pf[2];
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const float e = exp2f(s[v] - mnew);
+      const float e = softmax_exp2(s[v] - mnew);
       psum += e;
       pf[v >> 3][v & 7] = (_Float16)e;
     }
     psum += __shfl_xor(psum, 32, kWave);
     if (!__all(mnew == m_run)) {  // rescale only when some running maximum moved
-      const float alpha = exp2f(m_run - mnew);
+      const float alpha = softmax_exp2(m_run - mnew);
       l_run *= alpha;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {

@@ -29,9 +29,16 @@ COMMON = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}', '-Wall', '-Wno
           '-Wno-unused-variable', '-Wno-unused-but-set-variable'] + DEVICE_FLAGS
 
 
+# Per-file device flags.  attention.hip: the online softmax rescales the MFMA
+# accumulators with VALU instructions, so they must live in VGPRs; left to its
+# heuristics the compiler puts them in AGPRs and moves every value back and forth
+# (157 v_accvgpr moves per 32-key block in the fp16 kernel).
+FILE_FLAGS = {'attention.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form']}
+
+
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + '.o')
-    cmd = [HIPCC] + COMMON + ['-c', src, '-o', obj]
+    cmd = [HIPCC] + COMMON + FILE_FLAGS.get(os.path.basename(src), []) + ['-c', src, '-o', obj]
     if verbose:
         print(' '.join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
