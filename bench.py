@@ -68,7 +68,7 @@ def profiled_traffic(config: str):
     return None
 
 
-def cpu_baseline(tokens_cpu, pools_gpu, r_list, image_size, gpu_scores_rl0, budget_s: float = 20.0):
+def cpu_baseline(tokens_cpu, pools_gpu, r_list, image_size, gpu_scores_rl0, budget_s: float = 12.0):
     """Time the oracle (torch CPU restatement of the original backend) on a bounded sample.
 
     Sample: LNAMD (Unfold path) for one batch of 4 images, every layer and radius;
@@ -94,7 +94,8 @@ def cpu_baseline(tokens_cpu, pools_gpu, r_list, image_size, gpu_scores_rl0, budg
     z = pools_gpu[0, 0].cpu()
     z = z / z.norm(dim=-1, keepdim=True)      # the pools hold unnormalised window sums
     q_times, errs = [], []
-    queries = [0, n // 2, n - 1, 1, n // 3, 2 * n // 3, n - 2, 5]
+    # up to 48 query images spread over the pool, until the time budget is spent
+    queries = sorted(set(int(round(k * (n - 1) / 47)) for k in range(48)), key=lambda i: (i * 37) % n)
     spent = 0.0
     for i in queries:
         t1 = time.perf_counter()

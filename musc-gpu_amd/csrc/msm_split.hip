@@ -90,12 +90,42 @@ __global__ __launch_bounds__(256) void split_prepare_kernel(const float* __restr
   const double sc = acc > 0.0 ? ldexp(1.0 / sqrt(acc), kScaleShift) : 0.0;
   _Float16* dst = hl + row * (long long)nkb * (2 * KB);
   const int cp = nkb * KB;
-  for (int k = lane; k < cp; k += kWave) {
-    const double v = k < c ? (double)src[k] * sc : 0.0;
-    const _Float16 hi = (_Float16)(float)v;
-    const _Float16 lo = (_Float16)(float)(v - (double)(float)hi);
-    dst[(k / KB) * (2 * KB) + (k % KB)] = hi;
-    dst[(k / KB) * (2 * KB) + KB + (k % KB)] = lo;
+  auto split1 = [&](float x, _Float16& hi, _Float16& lo) {
+    const double v = (double)x * sc;
+    hi = (_Float16)(float)v;
+    lo = (_Float16)(float)(v - (double)(float)hi);
+  };
+  if ((c & 7) == 0) {
+    // eight channels per lane: one 16-byte store of hi and one of lo (half a
+    // 16-channel block each); c % 8 == 0 keeps every group inside one block
+    for (int k0 = 8 * lane; k0 < cp; k0 += 8 * kWave) {
+      half8 hi, lo;
+      if (k0 < c) {
+        const float4 x0 = *reinterpret_cast<const float4*>(src + k0);
+        const float4 x1 = *reinterpret_cast<const float4*>(src + k0 + 4);
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          _Float16 h, l;
+          split1(xs[j], h, l);
+          hi[j] = h;
+          lo[j] = l;
+        }
+      } else {
+        hi = half8{};
+        lo = half8{};
+      }
+      _Float16* blk = dst + (k0 / KB) * (2 * KB) + (k0 % KB);
+      *reinterpret_cast<half8*>(blk) = hi;
+      *reinterpret_cast<half8*>(blk + KB) = lo;
+    }
+  } else {
+    for (int k = lane; k < cp; k += kWave) {
+      _Float16 hi = (_Float16)0.f, lo = (_Float16)0.f;
+      if (k < c) split1(src[k], hi, lo);
+      dst[(k / KB) * (2 * KB) + (k % KB)] = hi;
+      dst[(k / KB) * (2 * KB) + KB + (k % KB)] = lo;
+    }
   }
 }
 
