@@ -202,14 +202,8 @@ def bench_attention(args):
     dev = torch.device('cuda:0')
     dtype = torch.float32 if args.dtype == 'fp32' else torch.float16
     B, H, T, D = 4, 16, 1370, 64
-    g = torch.Generator().manual_seed(42)
-    blocks = []
-    for k in range(args.blocks):
-        # seeded on the CPU, projected on the GPU (input generation only)
-        y = torch.randn((B * T, 1024), generator=g).to(dev)
-        w = (torch.randn((1024, 3 * 1024), generator=g) * 0.02).to(dev)
-        qkv = (y @ w).reshape(B, T, 3, H, D).permute(2, 0, 3, 1, 4).reshape(3, B * H, T, D)
-        blocks.append(tuple(x.contiguous().to(dev, dtype) for x in qkv))
+    blocks = [tuple(x.to(dtype) for x in qkv)
+              for qkv in synthetic.attention_blocks(args.blocks, B, H, T, D, device=dev)]
     ts = []
     for it in range(args.iters + 1):
         e0, e1 = _events()

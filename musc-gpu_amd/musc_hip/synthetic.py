@@ -8,6 +8,8 @@ oracle see bit-identical inputs; the caller moves them to the device.
                           N(0,1) (n, 1370, 1024) and one shared mu_l ~ N(0,1)^1024
                           (offset scale 1.0), seed = seed + l
   msm_features(n, p, c)   kernel-only pools: (n, p, c) iid N(0,1), L2-normalised rows
+  attention_blocks(...)   config 4: per block, tokens y ~ N(0,1) (B*T, 1024) projected by
+                          W ~ N(0, 0.02^2) (1024, 3*1024) into (B*H, T, 64) q, k, v
 """
 from __future__ import annotations
 
@@ -38,6 +40,19 @@ def pool_tokens(n: int = 83, layers: int = 4, tokens: int = 1370, c: int = 1024,
 def msm_features(n: int, p: int, c: int, seed: int = 42) -> torch.Tensor:
     g = torch.Generator().manual_seed(seed)
     return _normalise(torch.randn((n, p, c), generator=g, dtype=torch.float32))
+
+
+def attention_blocks(blocks: int = 24, b: int = 4, heads: int = 16, tokens: int = 1370, d: int = 64,
+                     seed: int = 42, device: torch.device | str = 'cpu'):
+    """Config 4: yields one (q, k, v) triple of fp32 (b*heads, tokens, d) tensors per block.
+    y and W are drawn on the CPU; the projection y @ W runs on `device`."""
+    g = torch.Generator().manual_seed(seed)
+    width = heads * d
+    for _ in range(blocks):
+        y = torch.randn((b * tokens, width), generator=g).to(device)
+        w = (torch.randn((width, 3 * width), generator=g) * 0.02).to(device)
+        qkv = (y @ w).reshape(b, tokens, 3, heads, d).permute(2, 0, 3, 1, 4).reshape(3, b * heads, tokens, d)
+        yield tuple(x.contiguous() for x in qkv)
 
 
 # CLIP image normalisation constants (OpenAI CLIP preprocessing)

@@ -1,8 +1,8 @@
-"""Fused attention parity on the GPU vs torch softmax(q k^T * scale) v computed on the CPU."""
+"""Fused attention parity on the GPU vs torch softmax(q k^T * scale) v (CPU fp32, or float64 for config 4)."""
 import pytest
 import torch
 
-from musc_hip import _attention_hip
+from musc_hip import _attention_hip, synthetic
 
 pytestmark = pytest.mark.gpu
 
@@ -39,3 +39,20 @@ def test_sharp_logits_select_one_row(device):
     v = torch.randn((1, t, 64))
     out = _attention_hip.attention(q.to(device), k.to(device), v.to(device), 1.0).cpu()
     torch.testing.assert_close(out[0], v[0, 37].expand(t, 64), rtol=0, atol=1e-5)
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float16])
+def test_config4_all_blocks(device, dtype):
+    # Config 4: B=4, T=1370, 16 heads of 64; q, k, v = N(0,1) tokens @ N(0, 0.02^2) weights,
+    # every one of the 24 blocks against softmax(q k^T / 8) v in float64 (on the GPU, from
+    # the same stored inputs).
+    tol = 2e-5 if dtype == torch.float32 else 2e-4
+    for blk, (q, k, v) in enumerate(synthetic.attention_blocks(24, device=device)):
+        q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+        out = _attention_hip.attention(q, k, v, 0.125)
+        q64, k64, v64 = q.double(), k.double(), v.double()
+        ref = torch.softmax(torch.bmm(q64 * 0.125, k64.transpose(1, 2).contiguous()), -1)
+        ref = torch.bmm(ref, v64)
+        err = (out.double() - ref).abs().max().item()
+        print(f'block {blk}: max |err| {err:.3e}', flush=True)
+        assert err <= tol + tol * ref.abs().max().item(), (blk, err)

@@ -68,6 +68,15 @@ def test_msm_rank_window_and_validation():
         _MSM_hip.MSM(torch.zeros((8, 4)))
 
 
+def test_msm_engine_selection():
+    _MSM_hip.check_engine('fp32', 1)
+    _MSM_hip.check_engine('split16', _MSM_hip.SPLIT_MIN_P)
+    with pytest.raises(ValueError, match='Unknown MSM engine'):
+        _MSM_hip.check_engine('bf16', 1369)
+    with pytest.raises(ValueError, match='P >= 256'):
+        _MSM_hip.check_engine('split16', _MSM_hip.SPLIT_MIN_P - 1)
+
+
 def test_aggregation_predicate():
     layer = _lnamd_hip.LNAMD(feature_dim=8, feature_layer=[1, 2], r=3)
     feats = [torch.zeros((2, 26, 8)), torch.zeros((2, 26, 8))]
