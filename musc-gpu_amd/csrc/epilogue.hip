@@ -94,9 +94,10 @@ extern "C" int musc_maps_f64(const double* scores, int n_radii, int n_layers, in
   // a band of kRows output rows touches at most floor(scale*(kRows-1)) + 3 grid rows
   const double scale = out_size > 1 ? (double)(side - 1) / (double)(out_size - 1) : 0.0;
   if ((int)(scale * (epi::kRows - 1)) + 3 > epi::kMaxGridRows) return MUSC_ERR_UNSUPPORTED;
+  const int bands = (out_size + epi::kRows - 1) / epi::kRows;
+  if ((long long)n * bands > 0x7fffffffLL) return MUSC_ERR_UNSUPPORTED;
   unsigned long long* bits = reinterpret_cast<unsigned long long*>(image_scores);
   if (bits) launch_fill_u32(reinterpret_cast<uint32_t*>(bits), (size_t)n * 2, 0u, stream);
-  const int bands = (out_size + epi::kRows - 1) / epi::kRows;
   hipLaunchKernelGGL(epi::maps_kernel, dim3((unsigned)(n * bands)), dim3(epi::kThreads), 0, stream, scores, n_radii,
                      n_layers, n, side, out_size, maps, bits);
   return check_launch();

@@ -745,6 +745,7 @@ extern "C" int musc_adaptive_pool_f32(const float* in, int batch, int side_in, i
   if (((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) != 0) return MUSC_ERR_INVALID_ARG;
   const long long total = (long long)batch * side_out * side_out * (ch / 4);
   if (total == 0) return MUSC_OK;
+  if ((total + 255) / 256 > 0x7fffffffLL) return MUSC_ERR_UNSUPPORTED;
   hipLaunchKernelGGL(lnamd::adaptive_pool_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, in,
                      batch, side_in, ch / 4, side_out, out);
   return check_launch();

@@ -505,11 +505,12 @@ __global__ __launch_bounds__(kRankWaves * kWave) void msm_rank_kernel(
 __global__ __launch_bounds__(256) void msm_nearest_kernel(const uint32_t* __restrict__ minbits,
                                                           size_t count, int n, int p,
                                                           float* __restrict__ nearest) {
-  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= count) return;
-  const size_t row = i / n;
-  const int j = (int)(i % n);
-  nearest[i] = (j == (int)(row / p)) ? __int_as_float(kInfBits) : sqrtf(__uint_as_float(minbits[i]));
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+    const size_t row = i / n;
+    const int j = (int)(i % n);
+    nearest[i] = (j == (int)(row / p)) ? __int_as_float(kInfBits) : sqrtf(__uint_as_float(minbits[i]));
+  }
 }
 
 inline int validate(const float* z, int n, int p, int c, void* ws, size_t ws_bytes) {
@@ -617,7 +618,8 @@ extern "C" int musc_msm_nearest_f32(const float* z, int n, int p, int c, float* 
   rc = msm::run_pairs(z, n, p, c, w, stream);
   if (rc) return rc;
   const size_t count = (size_t)n * p * n;
-  hipLaunchKernelGGL(msm::msm_nearest_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream,
-                     w.minbits, count, n, p, nearest);
+  const size_t blocks = (count + 255) / 256 < 65536 ? (count + 255) / 256 : 65536;  // grid-stride beyond
+  hipLaunchKernelGGL(msm::msm_nearest_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, w.minbits, count, n, p,
+                     nearest);
   return check_launch();
 }
