@@ -41,6 +41,40 @@ def test_random_shapes_vs_oracles(device, n, p, c):
     np.testing.assert_allclose(got, ref_64, rtol=0, atol=ATOL)
 
 
+@pytest.mark.parametrize('n,p,c', [(2, 1, 1), (2, 5, 3), (3, 1, 17), (4, 2, 5), (2, 130, 8)])
+def test_minimal_shapes(device, n, p, c):
+    # smallest pools (N = 2 needs topmin_max = 1 for a nonempty window), one patch per
+    # image, one channel; inputs spread out so no pair is within fp32 cancellation range
+    g = torch.Generator().manual_seed(n * 100 + p * 10 + c)
+    if c == 1:
+        z = torch.linspace(-1.0, 1.0, n * p)[torch.randperm(n * p, generator=g)].reshape(n, p, 1)
+    else:
+        z = torch.nn.functional.normalize(torch.randn((n, p, c), generator=g), dim=-1)
+    got = _MSM_hip.MSM(z.to(device), topmin_min=0, topmin_max=1.0).cpu().numpy()
+    ref = oracle.msm_scores_f64_c(z.numpy(), *om.rank_window(n, 0, 1.0))
+    np.testing.assert_allclose(got, ref, rtol=0, atol=ATOL)
+
+
+def test_closed_form_one_dimensional_offsets(device):
+    # Z[j] = base + delta_j * u: every patch's nearest patch in image j is the same patch,
+    # at |delta_j - delta_i|, so the scores are interval means of sorted |delta_j - delta_i|
+    rng = np.random.default_rng(14)
+    n, p, c = 11, 150, 64
+    base = rng.standard_normal((p, c))
+    base /= np.linalg.norm(base, axis=1, keepdims=True)
+    u = rng.standard_normal(c)
+    u /= np.linalg.norm(u)
+    # offsets at least 0.04 apart: the expanded form's ~1e-7 error in d^2 then stays far
+    # below the gate in d (it is not a property of the closed form but of fp32 cdist)
+    delta = rng.permutation((np.arange(n) + 0.5 * rng.random(n)) * 0.045)
+    z = (base[None] + delta[:, None, None] * u[None, None]).astype(np.float32)
+    got = _MSM_hip.MSM(torch.from_numpy(z).to(device)).cpu().numpy()
+    k_min, k_max = om.rank_window(n)
+    for i in range(n):
+        d = np.sort([abs(delta[j] - delta[i]) for j in range(n) if j != i])
+        np.testing.assert_allclose(got[i], d[k_min:k_max].mean(), rtol=0, atol=ATOL, err_msg=f'image {i}')
+
+
 def test_rank_windows(device):
     torch.manual_seed(3)
     z = torch.randn((21, 50, 24))

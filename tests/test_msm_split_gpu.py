@@ -36,6 +36,36 @@ def test_random_shapes_vs_oracles(device, n, p, c):
     np.testing.assert_allclose(got, ref_64, rtol=0, atol=ATOL)
 
 
+def test_two_image_pool(device):
+    # N = 2 (window [0, 1) with topmin_max = 1): every patch's score is its distance to the
+    # nearest patch of the other image
+    torch.manual_seed(5)
+    z = torch.nn.functional.normalize(torch.randn((2, 300, 48)), dim=-1)
+    got = _split(z.to(device), topmin_min=0, topmin_max=1.0).cpu().numpy()
+    ref = oracle.msm_scores_f64_c(z.numpy(), *om.rank_window(2, 0, 1.0))
+    np.testing.assert_allclose(got, ref, rtol=0, atol=ATOL)
+
+
+def test_closed_form_one_dimensional_offsets(device):
+    # Z[j] = base + delta_j * u (unnormalised rows): the nearest patch in image j is the
+    # same patch, at |delta_j - delta_i|
+    rng = np.random.default_rng(15)
+    n, p, c = 9, 260, 64
+    base = rng.standard_normal((p, c))
+    base /= np.linalg.norm(base, axis=1, keepdims=True)
+    u = rng.standard_normal(c)
+    u /= np.linalg.norm(u)
+    # offsets at least 0.04 apart: the expanded form's ~1e-7 error in d^2 then stays far
+    # below the gate in d (it is not a property of the closed form but of fp32 cdist)
+    delta = rng.permutation((np.arange(n) + 0.5 * rng.random(n)) * 0.045)
+    z = (base[None] + delta[:, None, None] * u[None, None]).astype(np.float32)
+    got = _split(torch.from_numpy(z).to(device)).cpu().numpy()
+    k_min, k_max = om.rank_window(n)
+    for i in range(n):
+        d = np.sort([abs(delta[j] - delta[i]) for j in range(n) if j != i])
+        np.testing.assert_allclose(got[i], d[k_min:k_max].mean(), rtol=0, atol=ATOL, err_msg=f'image {i}')
+
+
 def _split_minima(z: torch.Tensor, normalize: bool) -> np.ndarray:
     """Squared per-(row, image) minima left by the split pair kernel in its workspace."""
     n, p, c = z.shape
