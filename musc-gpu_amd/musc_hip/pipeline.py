@@ -52,42 +52,44 @@ def msm_all(pools: torch.Tensor, topmin_min: float = 0, topmin_max: float = 0.3,
     it runs on.  `engine` selects how the dot products are formed ('fp32' or
     'split16', see _MSM_hip).
     """
+    rt.require_device_tensor(pools, 'pools')
+    if pools.ndim != 5 or pools.dtype != torch.float32 or not pools.is_contiguous():
+        raise ValueError('pools must be a contiguous fp32 (R, L, N, P, C) tensor')
     r, l, n, p, c = pools.shape
     a, b = _MSM_hip.rank_window(n, topmin_min, topmin_max)
     if not 0 <= a < b <= n - 1:
         raise ValueError('Require valid nonempty trimmed ranks 0<=a<b<=N-1.')
-    if pools.dtype != torch.float32 or not pools.is_contiguous():
-        raise ValueError('pools must be a contiguous fp32 (R, L, N, P, C) tensor')
     _MSM_hip.check_engine(engine, p)
-    scores = torch.empty((r, l, n, p), dtype=torch.float64, device=pools.device)
-    ws = rt.workspace(_MSM_hip.workspace_bytes(n, p, c, engine), pools.device)
     lib = rt.library()
-    s = rt.stream(pools.device)
     flags = rt.MSM_NORMALIZE_ROWS if normalize_rows else 0
     split = engine == 'split16'
-    for ri in range(r):
-        for li in range(l):
-            z = pools[ri, li]
-            if split:
-                rt.check(lib.musc_msm_split_prepare_f32(z.data_ptr(), n, p, c, flags, ws.data_ptr(), ws.numel(), s),
-                         'musc_msm_split_prepare_f32')
-            else:
-                rt.check(lib.musc_msm_prepare_f32(z.data_ptr(), n, p, c, flags, ws.data_ptr(), ws.numel(), s),
-                         'musc_msm_prepare_f32')
-            if pair_events is not None:
-                ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                ev[0].record()
-            if split:
-                rt.check(lib.musc_msm_split_pair_minima(n, p, c, ws.data_ptr(), ws.numel(), s),
-                         'musc_msm_split_pair_minima')
-            else:
-                rt.check(lib.musc_msm_pair_minima_f32(z.data_ptr(), n, p, c, ws.data_ptr(), ws.numel(), s),
-                         'musc_msm_pair_minima_f32')
-            if pair_events is not None:
-                ev[1].record()
-                pair_events.append(ev)
-            rt.check(lib.musc_msm_rank_f32(n, p, a, b, scores[ri, li].data_ptr(), ws.data_ptr(), ws.numel(), s),
-                     'musc_msm_rank_f32')
+    with torch.cuda.device(pools.device):
+        scores = torch.empty((r, l, n, p), dtype=torch.float64, device=pools.device)
+        ws = rt.workspace(_MSM_hip.workspace_bytes(n, p, c, engine), pools.device)
+        s = rt.stream(pools.device)
+        for ri in range(r):
+            for li in range(l):
+                z = pools[ri, li]
+                if split:
+                    rt.check(lib.musc_msm_split_prepare_f32(z.data_ptr(), n, p, c, flags, ws.data_ptr(), ws.numel(),
+                                                            s), 'musc_msm_split_prepare_f32')
+                else:
+                    rt.check(lib.musc_msm_prepare_f32(z.data_ptr(), n, p, c, flags, ws.data_ptr(), ws.numel(), s),
+                             'musc_msm_prepare_f32')
+                if pair_events is not None:
+                    ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                    ev[0].record()
+                if split:
+                    rt.check(lib.musc_msm_split_pair_minima(n, p, c, ws.data_ptr(), ws.numel(), s),
+                             'musc_msm_split_pair_minima')
+                else:
+                    rt.check(lib.musc_msm_pair_minima_f32(z.data_ptr(), n, p, c, ws.data_ptr(), ws.numel(), s),
+                             'musc_msm_pair_minima_f32')
+                if pair_events is not None:
+                    ev[1].record()
+                    pair_events.append(ev)
+                rt.check(lib.musc_msm_rank_f32(n, p, a, b, scores[ri, li].data_ptr(), ws.data_ptr(), ws.numel(), s),
+                         'musc_msm_rank_f32')
     return scores
 
 

@@ -58,6 +58,13 @@ def test_product_entry_points_reject_cpu_tensors():
         _attention_hip.attention(*(torch.zeros((1, 4, 64)) for _ in range(3)), 0.125)
     with pytest.raises(ValueError):
         _epilogue_hip.maps_and_scores(torch.zeros((1, 1, 2, 25), dtype=torch.float64), 13)
+    from musc_hip import _layers_hip, _super_fast, pipeline
+    with pytest.raises(ValueError):
+        pipeline.msm_all(torch.zeros((1, 1, 8, 4, 4)))
+    with pytest.raises(ValueError):
+        _super_fast.adaptive_pool(torch.zeros((2, 1369, 1, 8)))
+    with pytest.raises(ValueError):
+        _layers_hip.activation_(torch.zeros((4, 8)), 0)
 
 
 def test_bench_refuses_several_gpus():
