@@ -218,6 +218,26 @@ int musc_rscin_f32(const float* cls_tokens, const double* image_scores, int n, i
                    const int* k_list, int n_k, float* out, hipStream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* Image preprocessing of the data path (decoded uint8 RGB -> encoder input). */
+/* ------------------------------------------------------------------------ */
+
+/* images  (batch, in_h, in_w, 3) uint8 RGB, interleaved (as decoded by PIL after
+ *         .convert("RGB"), datasets/mvtec.py:101);
+ * out     (batch, 3, out_h, out_w) float32: Resize((out_h, out_w), BICUBIC) with
+ *         Pillow's 8-bit fixed-point resampling, CenterCrop (identity at that size),
+ *         ToTensor (u8 / 255) and Normalize ((x - mean[c]) / std[c]), bit-identical to
+ *         the reference's evaluation transform run on the CPU
+ *         (models/backbone/open_clip/transform.py:118-133, Pillow==11.1.0);
+ * mean3, std3  host arrays of 3 floats (OPENAI_DATASET_MEAN / _STD for CLIP).
+ * Workspace: musc_preprocess_workspace_bytes (coefficient tables + the uint8 output
+ * of the horizontal pass).  Reduction factors up to 15.5 per axis (64 taps);
+ * MUSC_ERR_UNSUPPORTED beyond, or for batch, in_h or out_h above 65535. */
+int musc_preprocess_workspace_bytes(int batch, int in_h, int in_w, int out_h, int out_w, size_t* out);
+int musc_preprocess_u8(const uint8_t* images, int batch, int in_h, int in_w, int out_h, int out_w,
+                       const float* mean3, const float* std3, float* out, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* ViT block attention: out = softmax(q k^T * scale) v per (batch*head).      */
 /* ------------------------------------------------------------------------ */
 

@@ -60,6 +60,8 @@ SIGNATURES = {
     'musc_maps_f64': (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp]),
     'musc_adaptive_pool_f32': (_i, [_vp, _i, _i, _i, _i, _vp, _vp]),
     'musc_rscin_f32': (_i, [_vp, _vp, _i, _i, _vp, _i, _vp, _vp]),
+    'musc_preprocess_workspace_bytes': (_i, [_i, _i, _i, _i, _i, ctypes.POINTER(_sz)]),
+    'musc_preprocess_u8': (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
     'musc_attention_fwd': (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _vp]),
     'musc_attention_weights_workspace_bytes': (_i, [_i, _i, _i, ctypes.POINTER(_sz)]),
     'musc_attention_weights': (_i, [_vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _vp, _sz, _vp]),

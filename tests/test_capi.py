@@ -116,3 +116,24 @@ def test_maps_and_attention_argument_errors(lib):
     assert lib.musc_maps_f64(fake, 1, 1, 2, 500, 13, fake, None, None) == 1003
     assert lib.musc_attention_fwd(fake, fake, fake, fake, 0, 4, 10, 32, 0.125, None) == 1003
     assert lib.musc_attention_fwd(fake, fake, fake, fake, 7, 4, 10, 64, 0.125, None) == 1001
+
+
+def test_preprocess_workspace_and_argument_errors(lib):
+    out = ctypes.c_size_t()
+    assert lib.musc_preprocess_workspace_bytes(4, 1024, 1024, 518, 518, ctypes.byref(out)) == 0
+    align = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    # two tables of 518 bounds + 518 x 9 coefficients, then the horizontal pass's rows
+    # (every source row is read when shrinking 1024 -> 518)
+    tables = 2 * (align(518 * 8) + align(518 * 9 * 4))
+    assert out.value == tables + align(4 * 1024 * 518 * 3)
+    assert lib.musc_preprocess_workspace_bytes(2, 518, 518, 518, 518, ctypes.byref(out)) == 0
+    assert out.value == 2 * (align(518 * 8) + align(518 * 4))     # nothing resampled: no intermediate
+    assert lib.musc_preprocess_workspace_bytes(0, 10, 10, 5, 5, ctypes.byref(out)) == 1001
+    assert lib.musc_preprocess_workspace_bytes(1, 2000, 2000, 100, 100, ctypes.byref(out)) == 1003  # 20x: > 64 taps
+    fake = ctypes.c_void_p(256)
+    m = (ctypes.c_float * 3)(0.5, 0.5, 0.5)
+    s0 = (ctypes.c_float * 3)(1.0, 0.0, 1.0)
+    big = ctypes.c_size_t(1 << 40)
+    assert lib.musc_preprocess_u8(None, 1, 10, 10, 5, 5, m, m, fake, fake, big, None) == 1001
+    assert lib.musc_preprocess_u8(fake, 1, 10, 10, 5, 5, m, s0, fake, fake, big, None) == 1001   # zero std
+    assert lib.musc_preprocess_u8(fake, 1, 10, 10, 5, 5, m, m, fake, fake, ctypes.c_size_t(8), None) == 1002

@@ -258,3 +258,75 @@ def test_rscin_oracle_vs_bruteforce_and_closed_forms():
     np.testing.assert_allclose(orc.rscin(raw, list(cls), [1]), (raw - raw.min()) / (raw.max() - raw.min()), atol=1e-6)
     # 0 in k_list or no tokens: unchanged
     assert orc.rscin(raw, list(cls), [0, 1]) is raw and orc.rscin(raw, None, [1]) is raw
+
+
+# ---------------------------------------------------------------------------
+# Image preprocessing: Pillow's bicubic resampling restated (oracle.preprocess)
+# ---------------------------------------------------------------------------
+
+PIL_CASES = [((64, 64), (518, 518)), ((100, 80), (37, 41)), ((1024, 1024), (518, 518)), ((900, 900), (518, 518)),
+             ((33, 517), (33, 518)), ((517, 33), (518, 33)), ((40, 40), (40, 40)), ((7, 5), (300, 2)),
+             ((700, 840), (518, 518)), ((300, 3), (17, 3)), ((3, 3), (1, 1)), ((224, 224), (518, 518))]
+
+
+@pytest.mark.parametrize('src,dst', PIL_CASES)
+def test_preprocess_resize_matches_pillow(src, dst):
+    # Pillow itself is the pin: the restatement must reproduce Image.resize(BICUBIC) byte for byte
+    from PIL import Image
+    from oracle import preprocess as op
+    rng = np.random.default_rng(src[0] * 7 + dst[1])
+    h, w = src
+    img = rng.integers(0, 256, (h, w, 3), dtype=np.uint8)
+    img[: h // 2] = (np.arange(w)[None, :, None] * 7 % 256).astype(np.uint8)   # sharp edges: clipping
+    ref = np.asarray(Image.fromarray(img, 'RGB').resize((dst[1], dst[0]), Image.BICUBIC))
+    np.testing.assert_array_equal(op.resize_bicubic_u8(img, *dst), ref)
+
+
+def test_preprocess_coefficients_sum_to_one_and_planted_error_fails():
+    from oracle import preprocess as op
+    for n_in, n_out in ((1024, 518), (224, 518), (900, 518), (5, 5)):
+        bounds, kk, taps = op.coefficients(n_in, n_out)
+        assert taps == 2 * int(np.ceil(2 * max(n_in / n_out, 1.0))) + 1
+        sums = kk.sum(axis=1)
+        assert np.all(np.abs(sums - (1 << op.PRECISION_BITS)) <= taps)    # normalised up to rounding
+        assert np.all(bounds[:, 0] >= 0) and np.all(bounds.sum(axis=1) <= n_in)
+    # a plausible mistake (rounding the intermediate by truncation) must break the Pillow pin
+    from PIL import Image
+    rng = np.random.default_rng(3)
+    img = rng.integers(0, 256, (50, 60, 3), dtype=np.uint8)
+    ref = np.asarray(Image.fromarray(img, 'RGB').resize((23, 19), Image.BICUBIC))
+    bh, kh, _ = op.coefficients(60, 23)
+    acc = (img.astype(np.int64)[:, bh[5, 0]:bh[5, 0] + bh[5, 1], 0] * kh[5, :bh[5, 1]]).sum(axis=1)
+    assert not np.array_equal(np.clip(acc >> op.PRECISION_BITS, 0, 255),
+                              np.clip((acc + (1 << (op.PRECISION_BITS - 1))) >> op.PRECISION_BITS, 0, 255))
+    assert np.array_equal(op.resize_bicubic_u8(img, 19, 23), ref)
+
+
+def test_preprocess_to_tensor_normalize_rounding():
+    # ToTensor is u / 255 and Normalize (x - m) / s, each a correctly rounded float32
+    # operation (torch CPU).  Checked against exact rational arithmetic for every byte:
+    # each stage's result must be a float32 nearest to the exact value of that stage
+    # (a reciprocal multiply or a fused form would miss for some bytes).
+    from fractions import Fraction
+    from oracle import preprocess as op
+
+    def nearest(x: np.float32, exact: Fraction) -> bool:
+        up = np.nextafter(x, np.float32(np.inf))
+        dn = np.nextafter(x, np.float32(-np.inf))
+        e = abs(Fraction(float(x)) - exact)
+        return e <= abs(Fraction(float(up)) - exact) and e <= abs(Fraction(float(dn)) - exact)
+
+    img = np.arange(256, dtype=np.uint8).reshape(16, 16, 1).repeat(3, axis=2)
+    got = op.to_tensor_normalize(img).numpy()
+    plain = op.to_tensor_normalize(img, mean=(0.0, 0.0, 0.0), std=(1.0, 1.0, 1.0)).numpy()
+    for c in range(3):
+        m = np.float32(op.OPENAI_DATASET_MEAN[c])
+        sd = np.float32(op.OPENAI_DATASET_STD[c])
+        for u in range(256):
+            t = plain[c].reshape(-1)[u]
+            assert nearest(t, Fraction(u, 255)), u
+            r = np.float32(t - m)
+            assert nearest(r, Fraction(float(t)) - Fraction(float(m)))
+            d = got[c].reshape(-1)[u]
+            assert nearest(d, Fraction(float(r)) / Fraction(float(sd))), (c, u)
+    assert plain[:, 0, 0].tolist() == [0.0] * 3 and plain[:, -1, -1].tolist() == [1.0] * 3
