@@ -229,9 +229,12 @@ int musc_rscin_f32(const float* cls_tokens, const double* image_scores, int n, i
  *         the reference's evaluation transform run on the CPU
  *         (models/backbone/open_clip/transform.py:118-133, Pillow==11.1.0);
  * mean3, std3  host arrays of 3 floats (OPENAI_DATASET_MEAN / _STD for CLIP).
- * Workspace: musc_preprocess_workspace_bytes (coefficient tables + the uint8 output
- * of the horizontal pass).  Reduction factors up to 15.5 per axis (64 taps);
- * MUSC_ERR_UNSUPPORTED beyond, or for batch, in_h or out_h above 65535. */
+ * Workspace: musc_preprocess_workspace_bytes (coefficient tables, plus the uint8 output
+ * of the horizontal pass when both axes are resampled and the band of source rows does
+ * not fit the fused kernel's LDS, or in_w % 4 != 0).  When the fused kernel runs,
+ * images must be 4-byte aligned (MUSC_ERR_INVALID_ARG otherwise).  Reduction factors up
+ * to 15.5 per axis (64 taps); MUSC_ERR_UNSUPPORTED beyond, or for batch, in_h or out_h
+ * above 65535. */
 int musc_preprocess_workspace_bytes(int batch, int in_h, int in_w, int out_h, int out_w, size_t* out);
 int musc_preprocess_u8(const uint8_t* images, int batch, int in_h, int in_w, int out_h, int out_w,
                        const float* mean3, const float* std3, float* out, void* workspace,

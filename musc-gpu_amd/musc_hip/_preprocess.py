@@ -51,6 +51,8 @@ def preprocess_u8(images: torch.Tensor, size=518, mean=OPENAI_DATASET_MEAN, std=
     b, h, w, _ = x.shape
     oh, ow = _size(size)
     x = x.contiguous()
+    if x.data_ptr() % 16:
+        x = x.clone()             # the fused kernel reads 4-byte words; a fresh allocation is aligned
     lib = rt.library()
     with torch.cuda.device(x.device):
         if out is None:

@@ -9,6 +9,7 @@
     (msm, super_fast and e2e take --engine fp32|split16 for the MSM dot products)
     python musc-gpu_amd/musc_hip/kernels_bench.py mfma_peak                   (device calibration)
     python musc-gpu_amd/musc_hip/kernels_bench.py hbm                         (HBM calibration)
+    python musc-gpu_amd/musc_hip/kernels_bench.py preprocess --n 160 [--src 1024 --files 64]  (data path)
     python musc-gpu_amd/musc_hip/kernels_bench.py msm lnamd copy --iters 1   (several in one process)
 
 Each prints one JSON line with the average duration of the kernel(s) from HIP
@@ -22,11 +23,13 @@ import argparse
 import json
 import os
 import sys
+import time
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 if os.path.dirname(HERE) not in sys.path:
     sys.path.insert(0, os.path.dirname(HERE))
 
+import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 from musc_hip import _MSM_hip, _attention_hip, _lnamd_hip, synthetic  # noqa: E402
@@ -292,10 +295,115 @@ def bench_copy(args):
             'gbps_read_plus_write': 2 * n * 4 / (ms / 1e3) / 1e9}
 
 
+def _synthetic_photos(n: int, h: int, w: int, seed: int = 42) -> torch.Tensor:
+    """(n, h, w, 3) uint8: smooth gradients, a few rectangles and mild noise (compresses like a photo)."""
+    g = torch.Generator().manual_seed(seed)
+    yy = torch.linspace(0, 1, h)[:, None, None]
+    xx = torch.linspace(0, 1, w)[None, :, None]
+    out = torch.empty((n, h, w, 3), dtype=torch.uint8)
+    for i in range(n):
+        base = torch.rand((1, 1, 3), generator=g) * 160 + 40 * yy + 40 * xx
+        y0, x0 = (int(v) for v in torch.randint(0, min(h, w) // 2, (2,), generator=g))
+        base[y0:y0 + h // 4, x0:x0 + w // 4] += 50
+        base += torch.randn((h, w, 3), generator=g) * 4
+        out[i] = base.clamp(0, 255).round().to(torch.uint8)
+    return out
+
+
+def bench_preprocess(args):
+    """Data path: decoded uint8 RGB images resident in HBM -> the encoder's normalised
+    float32 batch (Pillow-exact bicubic resize + ToTensor + Normalize), against the reference's
+    per-item CPU transform (PIL resize + torch ToTensor / Normalize) on host threads; with
+    --files, also the whole loader (PNG decode in threads) in both forms."""
+    import concurrent.futures as cf
+    import os
+    import tempfile
+
+    from PIL import Image
+
+    from musc_hip import _loader, _preprocess
+    dev = torch.device('cuda:0')
+    n, h, w, size = args.n, args.src, args.src, 518
+    imgs = _synthetic_photos(n, h, w)
+    x = imgs.to(dev)
+    out = torch.empty((n, 3, size, size), dtype=torch.float32, device=dev)
+    ts = []
+    for it in range(args.iters + 1):
+        e0, e1 = _events()
+        e0.record()
+        _preprocess.preprocess_u8(x, size, out=out)
+        e1.record()
+        torch.cuda.synchronize()
+        if it > 0:
+            ts.append(e0.elapsed_time(e1))
+    ms = sum(ts) / len(ts)
+    algo = float(n) * (h * w * 3 + 3 * size * size * 4)
+    res = {'kernel': 'preprocess', 'images': n, 'src': [h, w], 'size': size, 'avg_ms': ms,
+           'images_per_s': n / (ms / 1e3), 'algorithmic_bytes': algo, 'gbps': algo / (ms / 1e3) / 1e9,
+           'frac_hbm_peak': algo / (ms / 1e3) / 1e9 / HBM_GBPS}
+    print('[preprocess] gpu timed', file=sys.stderr, flush=True)
+
+    mean = torch.tensor(_preprocess.OPENAI_DATASET_MEAN, dtype=torch.float32).view(-1, 1, 1)
+    std = torch.tensor(_preprocess.OPENAI_DATASET_STD, dtype=torch.float32).view(-1, 1, 1)
+
+    def cpu_transform(img: Image.Image) -> torch.Tensor:
+        # the reference's per-item transform: PIL bicubic resize, ToTensor, Normalize
+        r = img.resize((size, size), Image.BICUBIC)
+        t = torch.from_numpy(np.array(r)).permute(2, 0, 1).contiguous().to(torch.float32).div(255)
+        return t.sub(mean).div(std)
+
+    threads = args.workers
+    torch.set_num_threads(1)
+    sample = min(n, 32)
+    pil = [Image.fromarray(imgs[i].numpy(), 'RGB') for i in range(sample)]
+    with cf.ThreadPoolExecutor(threads) as pool:
+        list(pool.map(cpu_transform, pil[:threads]))
+        t0 = time.perf_counter()
+        cpu_out = list(pool.map(cpu_transform, pil))
+        dt = time.perf_counter() - t0
+    res['cpu_baseline'] = {'images_per_s': sample / dt, 'threads': threads, 'sample_images': sample,
+                           'kind': 'reference transform (Pillow resize + torch ToTensor/Normalize)'}
+    res['cpu_vs_gpu_max_abs_diff'] = max((cpu_out[i] - out[i].cpu()).abs().max().item() for i in range(sample))
+    print('[preprocess] cpu baseline timed', file=sys.stderr, flush=True)
+
+    if args.files:
+        with tempfile.TemporaryDirectory(dir=os.environ.get('TMPDIR', '/tmp')) as d:
+            paths = []
+            for i in range(args.files):
+                p = os.path.join(d, f'{i:04d}.png')
+                Image.fromarray(imgs[i % n].numpy(), 'RGB').save(p, compress_level=1)
+                paths.append(p)
+            print('[preprocess] files written', file=sys.stderr, flush=True)
+
+            class CpuItems(torch.utils.data.Dataset):
+                def __len__(self):
+                    return len(paths)
+
+                def __getitem__(self, i):
+                    with Image.open(paths[i]) as im:
+                        return {'image': cpu_transform(im.convert('RGB')), 'image_path': paths[i]}
+
+            t0 = time.perf_counter()
+            for b in _loader.ThreadedDatasetLoader(CpuItems(), 4, threads, pin_memory=True):
+                b['image'].to(dev, non_blocking=True)
+            torch.cuda.synchronize()
+            t_cpu = time.perf_counter() - t0
+            t0 = time.perf_counter()
+            for batch, _ in _loader.device_batches(paths, size, batch_size=4, workers=threads, device=dev):
+                pass
+            torch.cuda.synchronize()
+            t_gpu = time.perf_counter() - t0
+            res['loader'] = {'files': len(paths), 'format': 'PNG', 'workers': threads,
+                             'cpu_transform_images_per_s': len(paths) / t_cpu,
+                             'gpu_transform_images_per_s': len(paths) / t_gpu}
+            print('[preprocess] loaders timed', file=sys.stderr, flush=True)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('kernels', nargs='+', choices=['msm', 'lnamd', 'super_fast', 'attention', 'copy', 'e2e',
-                                                     'mfma_peak', 'hbm'])
+                                                     'mfma_peak', 'hbm', 'preprocess'])
     ap.add_argument('--n', type=int, default=83)
     ap.add_argument('--p', type=int, default=1369)
     ap.add_argument('--c', type=int, default=1024)
@@ -305,9 +413,13 @@ def main():
     ap.add_argument('--mib', type=int, default=1024)
     ap.add_argument('--iters', type=int, default=3)
     ap.add_argument('--engine', choices=['fp32', 'split16'], default='fp32', help='MSM dot-product engine')
+    ap.add_argument('--src', type=int, default=1024, help='preprocess: source image side')
+    ap.add_argument('--workers', type=int, default=4, help='preprocess: host threads (the reference loader uses 4)')
+    ap.add_argument('--files', type=int, default=0, help='preprocess: also time the loaders over this many PNG files')
     args = ap.parse_args()
     table = {'msm': bench_msm, 'lnamd': bench_lnamd, 'super_fast': bench_super_fast, 'attention': bench_attention,
-             'copy': bench_copy, 'e2e': bench_e2e, 'mfma_peak': bench_mfma_peak, 'hbm': bench_hbm}
+             'copy': bench_copy, 'e2e': bench_e2e, 'mfma_peak': bench_mfma_peak, 'hbm': bench_hbm,
+             'preprocess': bench_preprocess}
     for name in args.kernels:
         print(json.dumps(table[name](args)), flush=True)
 

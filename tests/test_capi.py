@@ -122,12 +122,14 @@ def test_preprocess_workspace_and_argument_errors(lib):
     out = ctypes.c_size_t()
     assert lib.musc_preprocess_workspace_bytes(4, 1024, 1024, 518, 518, ctypes.byref(out)) == 0
     align = lambda x: (x + 255) // 256 * 256  # noqa: E731
-    # two tables of 518 bounds + 518 x 9 coefficients, then the horizontal pass's rows
-    # (every source row is read when shrinking 1024 -> 518)
-    tables = 2 * (align(518 * 8) + align(518 * 9 * 4))
-    assert out.value == tables + align(4 * 1024 * 518 * 3)
+    # two tables of 518 bounds + 518 coefficient rows; 9 taps are stored 12 wide (the widths
+    # the kernels are instantiated for: 4, 8, 12, 16, 24, 32, 48, 64)
+    tables = 2 * (align(518 * 8) + align(518 * 12 * 4))
+    assert out.value == tables                          # fused kernel: the intermediate stays in LDS
+    assert lib.musc_preprocess_workspace_bytes(4, 1022, 1022, 518, 518, ctypes.byref(out)) == 0
+    assert out.value == tables + align(4 * 1022 * 518 * 3)   # in_w % 4 != 0: two passes through HBM
     assert lib.musc_preprocess_workspace_bytes(2, 518, 518, 518, 518, ctypes.byref(out)) == 0
-    assert out.value == 2 * (align(518 * 8) + align(518 * 4))     # nothing resampled: no intermediate
+    assert out.value == 2 * (align(518 * 8) + align(518 * 4 * 4))     # nothing resampled: no intermediate
     assert lib.musc_preprocess_workspace_bytes(0, 10, 10, 5, 5, ctypes.byref(out)) == 1001
     assert lib.musc_preprocess_workspace_bytes(1, 2000, 2000, 100, 100, ctypes.byref(out)) == 1003  # 20x: > 64 taps
     fake = ctypes.c_void_p(256)

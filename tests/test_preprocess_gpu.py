@@ -13,8 +13,11 @@ from musc_hip import _loader, _preprocess
 
 pytestmark = pytest.mark.gpu
 
+# fused band kernel: both axes resampled and in_w % 4 == 0 (1024, 900, 224, 700x840, 100x80, 3000x8);
+# two passes through HBM: in_w % 4 != 0 (1022, 7x5, 3x3) or one axis kept (33x517, 517x33, 518)
 CASES = [((1024, 1024), 518), ((900, 900), 518), ((224, 224), 518), ((518, 518), 518), ((700, 840), 518),
-         ((100, 80), (37, 41)), ((33, 517), (33, 518)), ((517, 33), (518, 33)), ((7, 5), (300, 2)), ((3, 3), 1)]
+         ((100, 80), (37, 41)), ((33, 517), (33, 518)), ((517, 33), (518, 33)), ((7, 5), (300, 2)), ((3, 3), 1),
+         ((1022, 1022), 518), ((3000, 8), (300, 5))]
 
 
 def _images(b, h, w, seed):
@@ -48,6 +51,17 @@ def test_resized_bytes_equal_pillow(device):
     for i in range(2):
         ref = np.asarray(Image.fromarray(imgs[i], 'RGB').resize((222, 300), Image.BICUBIC))
         np.testing.assert_array_equal(u8[i], ref)
+
+
+def test_unaligned_view_is_handled(device):
+    imgs = _images(2, 64, 48, 9)
+    flat = torch.zeros(imgs.size + 1, dtype=torch.uint8)
+    flat[1:] = torch.from_numpy(imgs.reshape(-1))
+    view = flat.to(device)[1:].view(2, 64, 48, 3)          # storage offset 1: not 4-byte aligned
+    assert view.data_ptr() % 4 != 0
+    got = _preprocess.preprocess_u8(view, 30).cpu()
+    ref = torch.stack([op.clip_preprocess(im, 30) for im in imgs], 0)
+    assert torch.equal(got, ref)
 
 
 def test_single_image_and_out_argument(device):
