@@ -194,12 +194,13 @@ __global__ __launch_bounds__(kThreads) void vpass_kernel(const uint8_t* __restri
 // ToTensor + Normalize then reads that block and writes the float32 planes.  The
 // uint8 intermediate never reaches HBM.  A thread owns output columns tid + 256 j
 // (j < kCols) in every row, so its horizontal coefficients are loaded into registers
-// once; the band's vertical coefficient rows sit in LDS.  Needs in_w % 4 == 0
-// (4-byte aligned rows), out_w <= 256 * kCols and kW <= 16; the host sizes `band`
-// and the dynamic LDS (fused_plan).
+// once; the band's vertical coefficient rows sit in LDS.  kT is the larger of the
+// two axes' tap counts (odd, <= 15), kW its coefficient row width.  Needs
+// in_w % 4 == 0 (4-byte aligned rows) and out_w <= 256 * kCols; the host sizes
+// `band` and the dynamic LDS (fused_plan).
 constexpr int kRowRegs = 16;     // 4-byte words per thread per staged row (in_w * 3 <= 16 KB)
 constexpr int kCols = 3;         // output columns per thread (out_w <= 768)
-constexpr int kFusedMaxW = 16;
+constexpr int kFusedMaxTaps = 15;
 
 struct FusedLayout {
   int rowpad;        // bytes per staged source row (x2 buffers), with slack for the widest window read
@@ -217,23 +218,25 @@ __host__ __device__ inline FusedLayout fused_layout(int in_w, int out_w, int nro
   return f;
 }
 
-// Horizontal tap sums of one output pixel from an LDS row: the window's 3*kW bytes
-// start at byte a; they are read as 3*kW/4 + 1 aligned 4-byte words, realigned by
-// a % 4 with v_alignbyte, and each byte is then at a compile-time position.
-template <int kW>
+// Horizontal tap sums of one output pixel from an LDS row: the window's 3*kT bytes
+// (kT = the axis' tap count, <= kW) start at byte a; they are read as aligned 4-byte
+// words, realigned by a % 4 with v_alignbyte, and each byte is then at a
+// compile-time position.
+template <int kW, int kT>
 __device__ inline int3 hsum_words(const uint8_t* __restrict__ row, int a, const int (&c)[kW]) {
-  constexpr int kD = 3 * kW / 4 + 1;
+  constexpr int kE = (3 * kT + 3) / 4;           // realigned words holding the 3*kT window bytes
+  constexpr int kD = kE + 1;                      // words read: the window at any offset a % 4
   const uint32_t* w = reinterpret_cast<const uint32_t*>(row + (a & ~3));
   uint32_t d[kD];
 #pragma unroll
   for (int i = 0; i < kD; ++i) d[i] = w[i];
   const uint32_t sh = (uint32_t)(a & 3);
-  uint32_t e[kD - 1];
+  uint32_t e[kE];
 #pragma unroll
-  for (int i = 0; i < kD - 1; ++i) e[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], sh);
+  for (int i = 0; i < kE; ++i) e[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], sh);
   int s0 = 1 << (kPrecisionBits - 1), s1 = s0, s2 = s0;
 #pragma unroll
-  for (int x = 0; x < kW; ++x) {
+  for (int x = 0; x < kT; ++x) {
     const int j = 3 * x;
     s0 += (int)((e[j >> 2] >> (8 * (j & 3))) & 0xffu) * c[x];
     s1 += (int)((e[(j + 1) >> 2] >> (8 * ((j + 1) & 3))) & 0xffu) * c[x];
@@ -242,7 +245,7 @@ __device__ inline int3 hsum_words(const uint8_t* __restrict__ row, int a, const 
   return make_int3(s0, s1, s2);
 }
 
-template <int kW>
+template <int kW, int kT>
 __global__ __launch_bounds__(kThreads) void fused_kernel(const uint8_t* __restrict__ src, int in_h, int in_w,
                                                          int out_h, int out_w, int band, int max_rows,
                                                          const int2* __restrict__ bh, const int* __restrict__ kh,
@@ -307,7 +310,7 @@ __global__ __launch_bounds__(kThreads) void fused_kernel(const uint8_t* __restri
       const int xx = tid + j * kThreads;
       if (xx < out_w) {
         // taps past the window carry weight 0; they read the row's slack bytes
-        const int3 s = hsum_words<kW>(row, hb[j].x * 3, hc[j]);
+        const int3 s = hsum_words<kW, kT>(row, hb[j].x * 3, hc[j]);
         dst[xx * 3 + 0] = (uint8_t)clip8(s.x);
         dst[xx * 3 + 1] = (uint8_t)clip8(s.y);
         dst[xx * 3 + 2] = (uint8_t)clip8(s.z);
@@ -331,7 +334,7 @@ __global__ __launch_bounds__(kThreads) void fused_kernel(const uint8_t* __restri
 #pragma unroll
     for (int q = 0; q < 12; ++q) acc[q] = 1 << (kPrecisionBits - 1);
 #pragma unroll
-    for (int y = 0; y < kW; ++y) {
+    for (int y = 0; y < kT; ++y) {
       const int rr = min(bd.x - r0 + y, nrows - 1);     // weight 0 past the window
       const uint32_t* w = reinterpret_cast<const uint32_t*>(blk + rr * f.bstride + x0 * 3);
       const uint32_t d[3] = {w[0], w[1], w[2]};
@@ -358,9 +361,9 @@ struct FusedPlan {
   size_t lds;
 };
 
-inline FusedPlan fused_plan(int in_h, int in_w, int out_h, int out_w, const AxisGeom& gv, int width) {
+inline FusedPlan fused_plan(int in_h, int in_w, int out_h, int out_w, const AxisGeom& gv, int taps, int width) {
   FusedPlan best{0, 0, 0};
-  if (in_w % 4 != 0 || in_w * 3 > kRowRegs * kThreads * 4 || out_w > kCols * kThreads || width > kFusedMaxW)
+  if (in_w % 4 != 0 || in_w * 3 > kRowRegs * kThreads * 4 || out_w > kCols * kThreads || taps > kFusedMaxTaps)
     return best;
   for (int band = 32; band >= 1; band /= 2) {
     int worst = 0;
@@ -391,6 +394,7 @@ struct Plan {
   int max_rows;              // fused kernel: most source rows a band reads
   size_t lds;                // fused kernel: dynamic LDS bytes
   int width;                 // coefficient row width (both axes): a bucket >= the taps of either axis
+  int taps;                  // the larger of the two axes' tap counts
   int row0, rows;            // source rows the vertical pass reads (horizontal pass extent)
   size_t off_bh, off_kh, off_bv, off_kv, off_tmp, total;
 };
@@ -403,8 +407,9 @@ inline Plan plan(int batch, int in_h, int in_w, int out_h, int out_w) {
   p.need_v = out_h != in_h;
   if (!p.need_h) p.gh.taps = 1;
   if (!p.need_v) p.gv.taps = 1;
-  p.width = table_width(p.gh.taps > p.gv.taps ? p.gh.taps : p.gv.taps);
-  const FusedPlan fp = (p.need_h && p.need_v) ? fused_plan(in_h, in_w, out_h, out_w, p.gv, p.width)
+  p.taps = p.gh.taps > p.gv.taps ? p.gh.taps : p.gv.taps;
+  p.width = table_width(p.taps);
+  const FusedPlan fp = (p.need_h && p.need_v) ? fused_plan(in_h, in_w, out_h, out_w, p.gv, p.taps, p.width)
                                               : FusedPlan{0, 0, 0};
   p.band = fp.band;
   p.max_rows = fp.max_rows;
@@ -483,12 +488,24 @@ extern "C" int musc_preprocess_u8(const uint8_t* images, int batch, int in_h, in
                      p.need_h ? 0 : 1, bh, kh);
   hipLaunchKernelGGL(prep::coeff_kernel, dim3((out_h + T - 1) / T), dim3(T), 0, stream, in_h, out_h, p.width,
                      vshift, p.need_v ? 0 : 1, bv, kv);
+  if (p.band > 0) {
+#define MUSC_PREP_FUSED(W, TAPS)                                                                                   \
+  hipLaunchKernelGGL((prep::fused_kernel<W, TAPS>), dim3((out_h + p.band - 1) / p.band, batch), dim3(T), p.lds,    \
+                     stream, images, in_h, in_w, out_h, out_w, p.band, p.max_rows, bh, kh, bv, kv, nrm, out)
+    switch (p.taps) {
+      case 1: case 3: case 5: MUSC_PREP_FUSED(8, 5); break;   // taps are odd; short windows use 5 (zero weights)
+      case 7: MUSC_PREP_FUSED(8, 7); break;
+      case 9: MUSC_PREP_FUSED(12, 9); break;
+      case 11: MUSC_PREP_FUSED(12, 11); break;
+      case 13: MUSC_PREP_FUSED(16, 13); break;
+      case 15: MUSC_PREP_FUSED(16, 15); break;
+      default: return MUSC_ERR_UNSUPPORTED;
+    }
+#undef MUSC_PREP_FUSED
+    return check_launch();
+  }
 #define MUSC_PREP_LAUNCH(W)                                                                                        \
-  if (W <= prep::kFusedMaxW && p.band > 0) {                                                                       \
-    hipLaunchKernelGGL(prep::fused_kernel<(W <= prep::kFusedMaxW ? W : 4)>, dim3((out_h + p.band - 1) / p.band,   \
-                       batch), dim3(T), p.lds, stream, images, in_h, in_w, out_h, out_w, p.band, p.max_rows, bh,  \
-                       kh, bv, kv, nrm, out);                                                                      \
-  } else if (p.need_h) {                                                                                           \
+  if (p.need_h) {                                                                                                  \
     hipLaunchKernelGGL(prep::hpass_kernel<W>, dim3((out_w + T - 1) / T, p.rows, batch), dim3(T), 0, stream,       \
                        images, tmp, in_h, in_w, p.row0, p.rows, out_w, bh, kh);                                     \
     hipLaunchKernelGGL(prep::vpass_kernel<W>, dim3((out_w + T - 1) / T, out_h, batch), dim3(T), 0, stream, tmp,   \

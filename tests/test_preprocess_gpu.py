@@ -13,11 +13,14 @@ from musc_hip import _loader, _preprocess
 
 pytestmark = pytest.mark.gpu
 
-# fused band kernel: both axes resampled and in_w % 4 == 0 (1024, 900, 224, 700x840, 100x80, 3000x8);
-# two passes through HBM: in_w % 4 != 0 (1022, 7x5, 3x3) or one axis kept (33x517, 517x33, 518)
+# fused band kernel (both axes resampled, in_w % 4 == 0), one case per tap count it is built
+# for: 5 (224 -> 518), 7 (600), 9 (1024, 900, 700x840), 11 (1100), 13 (100x80 -> 37x41), 15 (1700);
+# two passes through HBM: in_w % 4 != 0 (1022, 7x5, 3x3), one axis kept (33x517, 517x33, 518)
+# or more than 15 taps (3000x8 -> 300x5)
 CASES = [((1024, 1024), 518), ((900, 900), 518), ((224, 224), 518), ((518, 518), 518), ((700, 840), 518),
          ((100, 80), (37, 41)), ((33, 517), (33, 518)), ((517, 33), (518, 33)), ((7, 5), (300, 2)), ((3, 3), 1),
-         ((1022, 1022), 518), ((3000, 8), (300, 5))]
+         ((1022, 1022), 518), ((3000, 8), (300, 5)), ((600, 600), 518), ((1100, 1100), 518),
+         ((1700, 1700), 518)]
 
 
 def _images(b, h, w, seed):
