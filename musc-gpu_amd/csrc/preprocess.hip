@@ -352,8 +352,9 @@ __global__ __launch_bounds__(kThreads) void fused_kernel(const uint8_t* __restri
 
 // Band (output rows per workgroup) and LDS of the fused kernel, or band 0 when it does
 // not apply: the largest band (<= 32 rows) whose block fits 64 KB.  Larger bands
-// recompute fewer halo rows; measured at 1024 -> 518 the 64 KB choice (band 8, three
-// workgroups per CU) beat a 40 KB one (band 4, four per CU) by 6 %.
+// recompute fewer halo rows, smaller blocks let more workgroups share a CU; measured at
+// 1024 -> 518 the 64 KB choice (band 8, three workgroups per CU) beat both a 40 KB one
+// (band 4) and a 78 KB one (band 16, two per CU; 14 % slower).
 constexpr size_t kFusedLdsBudget = 64 * 1024;
 
 struct FusedPlan {
