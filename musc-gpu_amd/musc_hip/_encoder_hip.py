@@ -20,6 +20,9 @@ softmax.  Here, for the duration of the call, the forward of every block in
   nn.MultiheadAttention forward is replaced by in-projection -> fused attention ->
   out-projection.
 
+The tower's ln_pre and ln_post (the same cast-back LayerNorm) are swapped for the
+one-pass kernel too.
+
 Only block 12, whose weights Transformer.forward keeps (transformer.py:331-333),
 also returns head-averaged probabilities (musc_attention_weights_strided); other
 blocks return None for the weights, which their caller discards.  Calls that are
@@ -48,7 +51,8 @@ _STATS = {}
 
 def begin_inference():
     _STATS.clear()
-    _STATS.update(fused_blocks=0, fused_attention_calls=0, weight_blocks=0, fallback_calls=0, seconds=0.0)
+    _STATS.update(fused_blocks=0, fused_attention_calls=0, weight_blocks=0, fused_layer_norms=0, fallback_calls=0,
+                  seconds=0.0)
 
 
 def _count(key: str) -> None:
@@ -128,6 +132,18 @@ def _block_plan(block):
     return _activation_mode(act)
 
 
+def _fused_ln_forward(ln, original):
+    """ln_pre / ln_post of the vision tower (transformer.py:555-579; the cast-back LayerNorm
+    of :23-29) as one pass; other inputs keep the module's own forward."""
+    def forward(x):
+        if (isinstance(x, torch.Tensor) and x.is_cuda and not torch.is_grad_enabled()
+                and _layers_hip.supports_layer_norm(x.shape[-1], x.dtype)):
+            _count('fused_layer_norms')
+            return _layers_hip.layer_norm(x, ln.weight, ln.bias, ln.eps)
+        return original(x)
+    return forward
+
+
 def _fused_block_forward(block, original, mode: int, keep_weights: bool):
     ln_1, ln_2, attn = block.ln_1, block.ln_2, block.attn
     c_fc, c_proj = block.mlp.c_fc, block.mlp.c_proj
@@ -162,10 +178,16 @@ def _fused_block_forward(block, original, mode: int, keep_weights: bool):
 
 def encode_image(model, image, out_layers):
     """(pooled (B, D), [tokens (B, T, width)] for out_layers) with the fused blocks."""
-    blocks = getattr(getattr(getattr(model, 'visual', None), 'transformer', None), 'resblocks', [])
+    visual = getattr(model, 'visual', None)
+    blocks = getattr(getattr(visual, 'transformer', None), 'resblocks', [])
     restored = []
     start = time.perf_counter()
     try:
+        for name in ('ln_pre', 'ln_post'):
+            ln = getattr(visual, name, None)
+            if _cast_back_layer_norm(ln):
+                restored.append((ln, 'forward' in ln.__dict__, ln.__dict__.get('forward')))
+                ln.forward = _fused_ln_forward(ln, ln.forward)
         for index, block in enumerate(blocks):
             keep = (index == 11) or (len(blocks) < 12 and index == len(blocks) - 1)
             mode = _block_plan(block)

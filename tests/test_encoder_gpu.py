@@ -27,10 +27,11 @@ def test_fp32_tokens_match_math_path(device):
         torch.testing.assert_close(a, b, rtol=1e-4, atol=1e-5)
     stats = _encoder_hip.research_diagnostics()
     assert stats['fused_blocks'] == 4 and stats['fused_attention_calls'] == 4 and stats['weight_blocks'] == 1
-    assert stats['fallback_calls'] == 0
+    assert stats['fused_layer_norms'] == 2 and stats['fallback_calls'] == 0        # ln_pre, ln_post
     # the original forwards are restored
     for blk in model.visual.transformer.resblocks:
         assert 'forward' not in blk.__dict__ and 'forward' not in blk.attn.__dict__
+    assert 'forward' not in model.visual.ln_pre.__dict__ and 'forward' not in model.visual.ln_post.__dict__
 
 
 def test_autocast_fp16(device):
