@@ -5,7 +5,8 @@
 dataset items are produced by a thread pool, at most batch_size * prefetch_batches
 items are in flight, batches come out in dataset order, are collated like
 torch's DataLoader and pinned when pin_memory is set; a worker's exception surfaces
-in the consumer at its item, and leaving the iteration shuts the pool down.
+in the consumer at its item, and leaving the iteration shuts the pool down (items
+still queued are cancelled; the reference waits for them).
 
 The GPU variant of the data path moves the per-pixel work off the host:
 `DecodedImages` items are the decoded uint8 RGB arrays only (PIL decode and
@@ -64,13 +65,18 @@ class ThreadedDatasetLoader:
                     window.append(pool.submit(self.dataset.__getitem__, issued))
                     issued += 1
 
-            top_up()
-            while window:
-                take = min(self.batch_size, len(window))
-                samples = [window.popleft().result() for _ in range(take)]
+            try:
                 top_up()
-                batch = self.collate_fn(samples)
-                yield _pin(batch) if self.pin_memory else batch
+                while window:
+                    take = min(self.batch_size, len(window))
+                    samples = [window.popleft().result() for _ in range(take)]
+                    top_up()
+                    batch = self.collate_fn(samples)
+                    yield _pin(batch) if self.pin_memory else batch
+            finally:
+                # leaving early (break, exception): queued items are dropped, running ones finish
+                for future in window:
+                    future.cancel()
 
 
 class DecodedImages(torch.utils.data.Dataset):

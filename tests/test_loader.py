@@ -78,3 +78,21 @@ def test_decoded_images_and_collation(tmp_path):
     loader = _loader.ThreadedDatasetLoader(ds, batch_size=2, pin_memory=False, collate_fn=_loader.collate_images)
     out = list(loader)
     assert [b['image_path'] for b in out] == [paths[:2], paths[2:]]
+
+
+def test_leaving_early_cancels_queued_items():
+    import time
+
+    class Slow(Recording):
+        def __getitem__(self, i):
+            time.sleep(0.05)
+            return super().__getitem__(i)
+
+    ds = Slow(200)
+    loader = _loader.ThreadedDatasetLoader(ds, batch_size=4, workers=2, prefetch_batches=4, pin_memory=False)
+    it = iter(loader)
+    assert next(it)['i'].tolist() == [0, 1, 2, 3]
+    it.close()            # leaving the loop: the pool shuts down here
+    # 20 items were queued (16 in flight + 4 refilled); without cancelling, every one of them
+    # would be produced before the shutdown returns; with it, only the few already running
+    assert ds.max_requested < 10
