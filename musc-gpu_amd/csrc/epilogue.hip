@@ -91,9 +91,10 @@ extern "C" int musc_maps_f64(const double* scores, int n_radii, int n_layers, in
   if (!scores || n_radii < 1 || n_layers < 1 || n < 1 || side < 1 || out_size < 1) return MUSC_ERR_INVALID_ARG;
   if (!maps && !image_scores) return MUSC_ERR_INVALID_ARG;
   if (side > epi::kMaxSide) return MUSC_ERR_UNSUPPORTED;
-  // a band of kRows output rows touches at most floor(scale*(kRows-1)) + 3 grid rows
+  // a band of min(kRows, out_size) output rows touches at most floor(scale*(rows-1)) + 3 grid rows
   const double scale = out_size > 1 ? (double)(side - 1) / (double)(out_size - 1) : 0.0;
-  if ((int)(scale * (epi::kRows - 1)) + 3 > epi::kMaxGridRows) return MUSC_ERR_UNSUPPORTED;
+  const int band_rows = out_size < epi::kRows ? out_size : epi::kRows;
+  if ((int)(scale * (band_rows - 1)) + 3 > epi::kMaxGridRows) return MUSC_ERR_UNSUPPORTED;
   const int bands = (out_size + epi::kRows - 1) / epi::kRows;
   if ((long long)n * bands > 0x7fffffffLL) return MUSC_ERR_UNSUPPORTED;
   unsigned long long* bits = reinterpret_cast<unsigned long long*>(image_scores);
