@@ -5,7 +5,7 @@
     python musc-gpu_amd/musc_hip/kernels_bench.py attention [--dtype fp32|fp16 --blocks 24]
     python musc-gpu_amd/musc_hip/kernels_bench.py copy [--mib 1024 --iters 3]
     python musc-gpu_amd/musc_hip/kernels_bench.py super_fast [--n 83 --iters 3] (config 3 from tokens)
-    python musc-gpu_amd/musc_hip/kernels_bench.py e2e --n 160 --iters 1       (config 5)
+    python musc-gpu_amd/musc_hip/kernels_bench.py e2e --n 160 --iters 1       (config 5; --from-files: from PNGs)
     (msm, super_fast and e2e take --engine fp32|split16 for the MSM dot products)
     python musc-gpu_amd/musc_hip/kernels_bench.py mfma_peak                   (device calibration)
     python musc-gpu_amd/musc_hip/kernels_bench.py hbm                         (HBM calibration)
@@ -247,8 +247,46 @@ def bench_e2e(args):
         print(f'[e2e] iteration {it} done', file=sys.stderr, flush=True)
         del out
     enc, score, rsc, total = (sum(t[i] for t in ts) / len(ts) for i in range(4))
-    return {'kernel': 'e2e', 'engine': args.engine, 'n': args.n, 'encoder_ms': enc, 'lnamd_msm_epilogue_ms': score, 'rscin_ms': rsc,
-            'total_ms': total, 'images_per_s': args.n / (total / 1e3), 'anomalous_images': anomalous}
+    res = {'kernel': 'e2e', 'engine': args.engine, 'n': args.n, 'encoder_ms': enc, 'lnamd_msm_epilogue_ms': score,
+           'rscin_ms': rsc, 'total_ms': total, 'images_per_s': args.n / (total / 1e3), 'anomalous_images': anomalous}
+    if args.from_files:
+        res['from_files'] = _e2e_from_files(args, model, imgs, dev)
+    return res
+
+
+def _e2e_from_files(args, model, imgs, dev):
+    """The same images as 1024 x 1024 PNG files: threaded PIL decode, pinned uint8 batches,
+    GPU preprocessing to 518 (the evaluation transform), then run_category; wall clock."""
+    import tempfile
+
+    from PIL import Image
+
+    from musc_hip import _loader, pipeline
+    from musc_hip.synthetic import CLIP_MEAN, CLIP_STD
+    mean = torch.tensor(CLIP_MEAN, device=dev).view(1, 3, 1, 1)
+    std = torch.tensor(CLIP_STD, device=dev).view(1, 3, 1, 1)
+    rgb = ((imgs * std + mean).clamp(0, 1) * 255).round().to(torch.uint8)               # back to 8-bit RGB
+    rgb = torch.nn.functional.interpolate(rgb.float(), size=(1024, 1024), mode='nearest').to(torch.uint8)
+    rgb = rgb.permute(0, 2, 3, 1).contiguous().cpu().numpy()
+    with tempfile.TemporaryDirectory(dir=os.environ.get('TMPDIR', '/tmp')) as d:
+        paths = []
+        for i in range(rgb.shape[0]):
+            paths.append(os.path.join(d, f'{i:04d}.png'))
+            Image.fromarray(rgb[i], 'RGB').save(paths[-1], compress_level=1)
+        print('[e2e] PNG files written', file=sys.stderr, flush=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        batches = [b for b, _ in _loader.device_batches(paths, 518, batch_size=4, workers=args.workers, device=dev)]
+        images = torch.cat(batches, 0)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        out = pipeline.run_category(model, images, msm_engine=args.engine)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        del out
+    return {'files': len(paths), 'source': '1024x1024 PNG', 'workers': args.workers,
+            'load_decode_preprocess_s': t1 - t0, 'encoder_scoring_rscin_s': t2 - t1, 'total_s': t2 - t0,
+            'images_per_s': len(paths) / (t2 - t0)}
 
 
 def bench_mfma_peak(args):
@@ -416,6 +454,8 @@ def main():
     ap.add_argument('--src', type=int, default=1024, help='preprocess: source image side')
     ap.add_argument('--workers', type=int, default=4, help='preprocess: host threads (the reference loader uses 4)')
     ap.add_argument('--files', type=int, default=0, help='preprocess: also time the loaders over this many PNG files')
+    ap.add_argument('--from-files', action='store_true',
+                    help='e2e: also run the pipeline from 1024x1024 PNG files (decode, GPU preprocessing, scoring)')
     args = ap.parse_args()
     table = {'msm': bench_msm, 'lnamd': bench_lnamd, 'super_fast': bench_super_fast, 'attention': bench_attention,
              'copy': bench_copy, 'e2e': bench_e2e, 'mfma_peak': bench_mfma_peak, 'hbm': bench_hbm,
