@@ -35,6 +35,7 @@ constexpr int KPITCH = D + 4;       // K block row pitch (floats)
 // path (5 VALU instructions per exponential) is dropped.
 __device__ inline float softmax_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 constexpr int VPITCH = KB + 4;      // V^T block row pitch (floats)
+constexpr float kLazyLog2 = 8.f;    // running-maximum slack of the fp16 kernel's online softmax
 
 // Where head bh = b * heads + h of a (batch, heads, t, 64) tensor lives: element
 // (bh, row, d) is at b * sb + h * sh + row * st + d (strides in elements).  The
@@ -321,27 +322,31 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
 #pragma unroll
     for (int v = 1; v < 16; ++v) bmax = fmaxf(bmax, s[v]);
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
-    const float mnew = fmaxf(m_run, bmax);
-    float psum = 0.f;
-    half8 pf[2];
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const float e = softmax_exp2(s[v] - mnew);
-      psum += e;
-      pf[v >> 3][v & 7] = (_Float16)e;
-    }
-    psum += __shfl_xor(psum, 32, kWave);
-    if (!__all(mnew == m_run)) {  // rescale only when some running maximum moved
-      const float alpha = softmax_exp2(m_run - mnew);
+    // Lazy rescaling: the running maximum is only raised when some query's block maximum
+    // exceeds it by more than kLazyLog2, so the exponentials stay <= 2^kLazyLog2 (exact in
+    // fp16 range and fp32 sums) and the 33-multiply rescale runs on a few blocks, not on
+    // every block where any of the 32 queries sees a new maximum.
+    if (!__all(bmax <= m_run + kLazyLog2)) {
+      const float mnew = fmaxf(m_run, bmax);
+      const float alpha = softmax_exp2(m_run - mnew);  // 0 on the first block (m_run = -inf)
       l_run *= alpha;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         o0[v] *= alpha;
         o1[v] *= alpha;
       }
+      m_run = mnew;
     }
+    float psum = 0.f;
+    half8 pf[2];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const float e = softmax_exp2(s[v] - m_run);
+      psum += e;
+      pf[v >> 3][v & 7] = (_Float16)e;
+    }
+    psum += __shfl_xor(psum, 32, kWave);
     l_run += psum;
-    m_run = mnew;
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
       const half4 a0l = *reinterpret_cast<const half4*>(&Vt[buf][lq * VP16 + 16 * mm + 4 * lh]);
