@@ -35,7 +35,23 @@ constexpr int KPITCH = D + 4;       // K block row pitch (floats)
 // path (5 VALU instructions per exponential) is dropped.
 __device__ inline float softmax_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 constexpr int VPITCH = KB + 4;      // V^T block row pitch (floats)
-constexpr float kLazyLog2 = 8.f;    // running-maximum slack of the fp16 kernel's online softmax
+constexpr float kLazyLog2 = 8.f;    // running-maximum slack of the online softmax (exponentials <= 2^8)
+
+// max / sum of a value and its partner 32 lanes away (the two halves of a wave hold
+// the same query): v_permlane32_swap exchanges the halves in a VALU instruction, where
+// a shuffle would go through LDS, and both swapped copies feed one symmetric operation.
+__device__ inline float2 swap_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float halves_max(float v) {
+  const float2 p = swap_halves(v);
+  return fmaxf(p.x, p.y);
+}
+__device__ inline float halves_sum(float v) {
+  const float2 p = swap_halves(v);
+  return p.x + p.y;
+}
 
 // Where head bh = b * heads + h of a (batch, heads, t, 64) tensor lives: element
 // (bh, row, d) is at b * sb + h * sh + row * st + d (strides in elements).  The
@@ -169,16 +185,10 @@ __global__ __launch_bounds__(WAVES * kWave, 3) void attn_fwd_kernel(const float*
     float bmax = s[0];
 #pragma unroll
     for (int v = 1; v < 16; ++v) bmax = fmaxf(bmax, s[v]);
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
-    const float mnew = fmaxf(m, bmax);
-    float psum = 0.f;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      s[v] = softmax_exp2(s[v] - mnew);
-      psum += s[v];
-    }
-    psum += __shfl_xor(psum, 32, kWave);
-    if (!__all(mnew == m)) {  // rescale only when some running maximum moved
+    bmax = halves_max(bmax);
+    // lazy rescaling, as in the fp16 kernel: the running maximum moves only past kLazyLog2
+    if (!__all(bmax <= m + kLazyLog2)) {
+      const float mnew = fmaxf(m, bmax);
       const float alpha = softmax_exp2(m - mnew);  // 0 on the first block (m = -inf)
       l *= alpha;
 #pragma unroll
@@ -186,9 +196,16 @@ __global__ __launch_bounds__(WAVES * kWave, 3) void attn_fwd_kernel(const float*
         o0[v] *= alpha;
         o1[v] *= alpha;
       }
+      m = mnew;
     }
+    float psum = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      s[v] = softmax_exp2(s[v] - m);
+      psum += s[v];
+    }
+    psum = halves_sum(psum);
     l += psum;
-    m = mnew;
     // O^T += V^T P^T ; step e uses key 8*(e/4) + 4h + e%4 = register e of s
     const float* vrow0 = &Vt[buf][lq * VPITCH + 4 * lh];
     const float* vrow1 = &Vt[buf][(32 + lq) * VPITCH + 4 * lh];
@@ -321,7 +338,7 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
     float bmax = s[0];
 #pragma unroll
     for (int v = 1; v < 16; ++v) bmax = fmaxf(bmax, s[v]);
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+    bmax = halves_max(bmax);
     // Lazy rescaling: the running maximum is only raised when some query's block maximum
     // exceeds it by more than kLazyLog2, so the exponentials stay <= 2^kLazyLog2 (exact in
     // fp16 range and fp32 sums) and the 33-multiply rescale runs on a few blocks, not on
@@ -345,7 +362,7 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
       psum += e;
       pf[v >> 3][v & 7] = (_Float16)e;
     }
-    psum += __shfl_xor(psum, 32, kWave);
+    psum = halves_sum(psum);
     l_run += psum;
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
@@ -472,12 +489,12 @@ __global__ __launch_bounds__(kWave) void attn_wstats_kernel(const void* __restri
     float bmax = s[0];
 #pragma unroll
     for (int v = 1; v < 16; ++v) bmax = fmaxf(bmax, s[v]);
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, kWave));
+    bmax = halves_max(bmax);
     const float mnew = fmaxf(m_run, bmax);
     float psum = 0.f;
 #pragma unroll
     for (int v = 0; v < 16; ++v) psum += exp2f(s[v] - mnew);
-    psum += __shfl_xor(psum, 32, kWave);
+    psum = halves_sum(psum);
     l_run = l_run * exp2f(m_run - mnew) + psum;
     m_run = mnew;
   }
