@@ -16,6 +16,8 @@
 // (128 queries) of a workgroup.
 #include <hip/hip_fp16.h>
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace musc {
@@ -304,45 +306,63 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
     if (gk < t) r = *reinterpret_cast<const half4*>(vg + head + (long long)gk * st + 4 * dg);
     return r;
   };
-  half8 kreg = load_k(0);
-  half4 v0 = load_v(0, 0), v1 = load_v(0, 1);
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int buf = kb & 1;
-    *reinterpret_cast<half8*>(&Ks[buf][skey * KP16 + sd8]) = kreg;
+  auto store_k = [&](int buf, half8 kr) { *reinterpret_cast<half8*>(&Ks[buf][skey * KP16 + sd8]) = kr; };
+  auto store_v = [&](int buf, half4 a, half4 b) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-      half2v pr = {v0[i], v1[i]};
+      half2v pr = {a[i], b[i]};
       *reinterpret_cast<half2v*>(&Vt[buf][(4 * dg + i) * VP16 + 2 * kp]) = pr;
     }
-    if (kb + 1 < nkb) {
-      kreg = load_k(kb + 1);
+  };
+  // S^T of one staged key block (4 MFMAs over d = 64)
+  auto logits = [&](int buf) -> floatx16 {
+    floatx16 r;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) r[v] = 0.f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const half8 a = *reinterpret_cast<const half8*>(&Ks[buf][lq * KP16 + 16 * m + 8 * lh]);
+      r = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[m], r, 0, 0, 0);
+    }
+    return r;
+  };
+
+  // Software-pipelined key loop: iteration kb issues the logits MFMAs of block kb+1
+  // beside the softmax of block kb and its P V MFMAs, so each wave has independent
+  // matrix work while its exponentials and conversions run (this kernel has only
+  // ~2.75 waves per SIMD to hide that chain).  LDS holds K one block ahead of V.
+  half8 kreg = load_k(0);
+  store_k(0, kreg);
+  half4 v0 = load_v(0, 0), v1 = load_v(0, 1);
+  if (nkb > 1) kreg = load_k(1);
+  __syncthreads();
+  floatx16 s = logits(0);
+
+  auto step = [&](int kb, auto more_c) {
+    constexpr bool kMore = decltype(more_c)::value;
+    if constexpr (kMore) store_k((kb + 1) & 1, kreg);
+    store_v(kb & 1, v0, v1);
+    if constexpr (kMore) {
+      if (kb + 2 < nkb) kreg = load_k(kb + 2);
       v0 = load_v(kb + 1, 0);
       v1 = load_v(kb + 1, 1);
     }
     __syncthreads();
-
-    floatx16 s;
+    floatx16 sn;
+    if constexpr (kMore) sn = logits((kb + 1) & 1);
+    if constexpr (!kMore) {
+      if ((kb + 1) * KB > t) {  // only the last block is ragged
 #pragma unroll
-    for (int v = 0; v < 16; ++v) s[v] = 0.f;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const half8 a = *reinterpret_cast<const half8*>(&Ks[buf][lq * KP16 + 16 * m + 8 * lh]);
-      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[m], s, 0, 0, 0);
-    }
-    if ((kb + 1) * KB > t) {  // only the last block is ragged
-#pragma unroll
-      for (int v = 0; v < 16; ++v)
-        if (kb * KB + (v >> 2) * 8 + lh * 4 + (v & 3) >= t) s[v] = -INFINITY;
+        for (int v = 0; v < 16; ++v)
+          if (kb * KB + (v >> 2) * 8 + lh * 4 + (v & 3) >= t) s[v] = -INFINITY;
+      }
     }
     float bmax = s[0];
 #pragma unroll
     for (int v = 1; v < 16; ++v) bmax = fmaxf(bmax, s[v]);
     bmax = halves_max(bmax);
-    // Lazy rescaling: the running maximum is only raised when some query's block maximum
-    // exceeds it by more than kLazyLog2, so the exponentials stay <= 2^kLazyLog2 (exact in
-    // fp16 range and fp32 sums) and the 33-multiply rescale runs on a few blocks, not on
-    // every block where any of the 32 queries sees a new maximum.
+    // lazy rescaling (see kLazyLog2)
     if (!__all(bmax <= m_run + kLazyLog2)) {
       const float mnew = fmaxf(m_run, bmax);
       const float alpha = softmax_exp2(m_run - mnew);  // 0 on the first block (m_run = -inf)
@@ -364,18 +384,22 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
     }
     psum = halves_sum(psum);
     l_run += psum;
+    const int vb = kb & 1;
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
-      const half4 a0l = *reinterpret_cast<const half4*>(&Vt[buf][lq * VP16 + 16 * mm + 4 * lh]);
-      const half4 a0h = *reinterpret_cast<const half4*>(&Vt[buf][lq * VP16 + 16 * mm + 8 + 4 * lh]);
-      const half4 a1l = *reinterpret_cast<const half4*>(&Vt[buf][(32 + lq) * VP16 + 16 * mm + 4 * lh]);
-      const half4 a1h = *reinterpret_cast<const half4*>(&Vt[buf][(32 + lq) * VP16 + 16 * mm + 8 + 4 * lh]);
+      const half4 a0l = *reinterpret_cast<const half4*>(&Vt[vb][lq * VP16 + 16 * mm + 4 * lh]);
+      const half4 a0h = *reinterpret_cast<const half4*>(&Vt[vb][lq * VP16 + 16 * mm + 8 + 4 * lh]);
+      const half4 a1l = *reinterpret_cast<const half4*>(&Vt[vb][(32 + lq) * VP16 + 16 * mm + 4 * lh]);
+      const half4 a1h = *reinterpret_cast<const half4*>(&Vt[vb][(32 + lq) * VP16 + 16 * mm + 8 + 4 * lh]);
       const half8 a0 = {a0l[0], a0l[1], a0l[2], a0l[3], a0h[0], a0h[1], a0h[2], a0h[3]};
       const half8 a1 = {a1l[0], a1l[1], a1l[2], a1l[3], a1h[0], a1h[1], a1h[2], a1h[3]};
       o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, pf[mm], o0, 0, 0, 0);
       o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, pf[mm], o1, 0, 0, 0);
     }
-  }
+    if constexpr (kMore) s = sn;
+  };
+  for (int kb = 0; kb + 1 < nkb; ++kb) step(kb, std::integral_constant<bool, true>{});
+  step(nkb - 1, std::integral_constant<bool, false>{});
 
   if (q < t) {
     const float inv = 1.f / l_run;
