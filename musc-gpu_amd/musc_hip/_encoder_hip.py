@@ -21,7 +21,12 @@ softmax.  Here, for the duration of the call, the forward of every block in
   out-projection.
 
 The tower's ln_pre and ln_post (the same cast-back LayerNorm) are swapped for the
-one-pass kernel too.
+one-pass kernel too, and the patch embedding conv1 (transformer.py:380, :566: a
+Conv2d whose kernel equals its stride) becomes what it computes, a GEMM of the
+image's non-overlapping patches: one gather of the patches into (B * grid^2,
+3 * p^2) rows in the compute dtype, then torch's GEMM (hipBLASLt).  The convolution
+library chooses its algorithm per shape and, without a tuned database, can fall
+back to a direct convolution 60x slower than the GEMM.
 
 Only block 12, whose weights Transformer.forward keeps (transformer.py:331-333),
 also returns head-averaged probabilities (musc_attention_weights_strided); other
@@ -51,8 +56,8 @@ _STATS = {}
 
 def begin_inference():
     _STATS.clear()
-    _STATS.update(fused_blocks=0, fused_attention_calls=0, weight_blocks=0, fused_layer_norms=0, fallback_calls=0,
-                  seconds=0.0)
+    _STATS.update(fused_blocks=0, fused_attention_calls=0, weight_blocks=0, fused_layer_norms=0, patch_embeds=0,
+                  fallback_calls=0, seconds=0.0)
 
 
 def _count(key: str) -> None:
@@ -144,6 +149,34 @@ def _fused_ln_forward(ln, original):
     return forward
 
 
+def _patch_conv(conv) -> bool:
+    """A bias-free or biased Conv2d that tiles its input into non-overlapping patches."""
+    return (isinstance(conv, nn.Conv2d) and tuple(conv.kernel_size) == tuple(conv.stride)
+            and tuple(conv.dilation) == (1, 1) and conv.groups == 1 and conv.padding_mode == 'zeros'
+            and not isinstance(conv.padding, str) and tuple(conv.padding) == (0, 0))
+
+
+def _patch_embed_forward(conv, original):
+    """conv1 of the vision tower as patches @ weight^T.  Rows and columns the stride does
+    not reach are dropped, as the convolution drops them; under autocast the patches are
+    gathered already in the autocast dtype (the GEMM would cast them anyway)."""
+    ph, pw = conv.kernel_size
+
+    def forward(x):
+        if not (isinstance(x, torch.Tensor) and x.is_cuda and x.ndim == 4 and x.shape[1] == conv.in_channels
+                and x.shape[2] >= ph and x.shape[3] >= pw and not torch.is_grad_enabled()):
+            return original(x)
+        b, c = x.shape[:2]
+        gh, gw = x.shape[2] // ph, x.shape[3] // pw
+        dtype = torch.get_autocast_dtype('cuda') if torch.is_autocast_enabled('cuda') else x.dtype
+        patches = torch.empty((b, gh, gw, c, ph, pw), dtype=dtype, device=x.device)
+        patches.copy_(x[:, :, :gh * ph, :gw * pw].reshape(b, c, gh, ph, gw, pw).permute(0, 2, 4, 1, 3, 5))
+        out = F.linear(patches.view(b * gh * gw, c * ph * pw), conv.weight.reshape(conv.out_channels, -1), conv.bias)
+        _count('patch_embeds')
+        return out.view(b, gh, gw, conv.out_channels).permute(0, 3, 1, 2)     # (B, width, grid, grid)
+    return forward
+
+
 def _fused_block_forward(block, original, mode: int, keep_weights: bool):
     ln_1, ln_2, attn = block.ln_1, block.ln_2, block.attn
     c_fc, c_proj = block.mlp.c_fc, block.mlp.c_proj
@@ -188,6 +221,10 @@ def encode_image(model, image, out_layers):
             if _cast_back_layer_norm(ln):
                 restored.append((ln, 'forward' in ln.__dict__, ln.__dict__.get('forward')))
                 ln.forward = _fused_ln_forward(ln, ln.forward)
+        conv1 = getattr(visual, 'conv1', None)
+        if _patch_conv(conv1):
+            restored.append((conv1, 'forward' in conv1.__dict__, conv1.__dict__.get('forward')))
+            conv1.forward = _patch_embed_forward(conv1, conv1.forward)
         for index, block in enumerate(blocks):
             keep = (index == 11) or (len(blocks) < 12 and index == len(blocks) - 1)
             mode = _block_plan(block)

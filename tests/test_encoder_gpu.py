@@ -28,10 +28,33 @@ def test_fp32_tokens_match_math_path(device):
     stats = _encoder_hip.research_diagnostics()
     assert stats['fused_blocks'] == 4 and stats['fused_attention_calls'] == 4 and stats['weight_blocks'] == 1
     assert stats['fused_layer_norms'] == 2 and stats['fallback_calls'] == 0        # ln_pre, ln_post
+    assert stats['patch_embeds'] == 1
     # the original forwards are restored
     for blk in model.visual.transformer.resblocks:
         assert 'forward' not in blk.__dict__ and 'forward' not in blk.attn.__dict__
     assert 'forward' not in model.visual.ln_pre.__dict__ and 'forward' not in model.visual.ln_post.__dict__
+    assert 'forward' not in model.visual.conv1.__dict__
+
+
+@pytest.mark.parametrize('hw', [(56, 56), (518, 518), (31, 44)])
+@pytest.mark.parametrize('autocast', [False, True])
+def test_patch_embedding_gemm_matches_conv(device, hw, autocast):
+    # conv1 with kernel == stride as patches @ W^T; (31, 44): the rows and columns past
+    # the last whole patch are dropped, as the convolution drops them
+    torch.manual_seed(5)
+    conv = torch.nn.Conv2d(3, 96, kernel_size=14, stride=14, bias=False).to(device)
+    biased = torch.nn.Conv2d(3, 96, kernel_size=14, stride=14, bias=True).to(device)
+    x = torch.rand((3, 3) + hw, generator=torch.Generator().manual_seed(6)).to(device)
+    for m in (conv, biased):
+        assert _encoder_hip._patch_conv(m)
+        hook = _encoder_hip._patch_embed_forward(m, m.forward)
+        with torch.no_grad(), torch.autocast('cuda', dtype=torch.float16, enabled=autocast):
+            ref, got = m(x), hook(x)
+        assert got.shape == ref.shape and got.dtype == ref.dtype
+        tol = dict(rtol=2e-3, atol=2e-3) if autocast else dict(rtol=1e-5, atol=1e-5)
+        torch.testing.assert_close(got.float(), ref.float(), **tol)
+    assert not _encoder_hip._patch_conv(torch.nn.Conv2d(3, 8, kernel_size=14, stride=7))
+    assert not _encoder_hip._patch_conv(torch.nn.Conv2d(3, 8, kernel_size=14, stride=14, padding=1))
 
 
 def test_autocast_fp16(device):
