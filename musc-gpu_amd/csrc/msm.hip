@@ -64,18 +64,25 @@ __global__ __launch_bounds__(256) void msm_norms_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 // Pairwise minima on fp32 MFMA.
 // ---------------------------------------------------------------------------
-template <bool kVec4>
+// Staged operand registers are a native vector type: HIP's float4 is a struct, and
+// assigning one loaded from global memory into an array element is an aggregate copy
+// that the compiler left in scratch memory for the whole-chunk path.
+typedef float stage4 __attribute__((ext_vector_type(4)));
+
+// Operand loads: kLoad 2 = whole chunks (c a multiple of 2 * BK: no channel mask),
+// 1 = 16-byte loads with a channel mask (c % 4 == 0), 0 = scalar loads.
+template <int kLoad>
 __device__ inline void load_chunk(const float* __restrict__ z, int rows, int c, int row0, int k0,
-                                  float4 (&reg)[4]) {
+                                  stage4 (&reg)[4]) {
   const int t = threadIdx.x;
   const int lrow = t / (BK / 4);
   const int lk = (t % (BK / 4)) * 4;
-  if (kVec4 && (c % BK) == 0) {
-    // whole chunks: no channel mask; padded rows re-read the last row (masked later)
+  if constexpr (kLoad == 2) {
+    // padded rows re-read the last row (masked later)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = min(row0 + lrow + 32 * i, rows - 1);
-      reg[i] = *reinterpret_cast<const float4*>(z + (long long)r * c + k0 + lk);
+      reg[i] = *reinterpret_cast<const stage4*>(z + (long long)r * c + k0 + lk);
     }
     return;
   }
@@ -83,11 +90,11 @@ __device__ inline void load_chunk(const float* __restrict__ z, int rows, int c, 
   for (int i = 0; i < 4; ++i) {
     const int r = row0 + lrow + 32 * i;
     const int k = k0 + lk;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    stage4 v = {0.f, 0.f, 0.f, 0.f};
     if (r < rows) {
       const float* src = z + (long long)r * c + k;
-      if (kVec4) {
-        if (k < c) v = *reinterpret_cast<const float4*>(src);
+      if constexpr (kLoad == 1) {
+        if (k < c) v = *reinterpret_cast<const stage4*>(src);
       } else {
         if (k + 0 < c) v.x = src[0];
         if (k + 1 < c) v.y = src[1];
@@ -99,19 +106,19 @@ __device__ inline void load_chunk(const float* __restrict__ z, int rows, int c, 
   }
 }
 
-__device__ inline void store_chunk(float* __restrict__ dst, const float4 (&reg)[4]) {
+__device__ inline void store_chunk(float* __restrict__ dst, const stage4 (&reg)[4]) {
   const int t = threadIdx.x;
   const int lrow = t / (BK / 4);
   const int lk = (t % (BK / 4)) * 4;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    *reinterpret_cast<float4*>(dst + (lrow + 32 * i) * PITCH + lk) = reg[i];
+    *reinterpret_cast<stage4*>(dst + (lrow + 32 * i) * PITCH + lk) = reg[i];
 }
 
 // kSplit (p >= BM): a 128-row or 128-column range holds at most one image boundary,
 // so tiles straddling a boundary reduce in registers too, with two image segments
 // per dimension; otherwise (small p) they go through the LDS epilogue.
-template <bool kVec4, bool kSplit>
+template <int kLoad, bool kSplit>
 __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
     const float* __restrict__ z, const float* __restrict__ norms, const float* __restrict__ inv,
     uint32_t* __restrict__ minbits, int rows, int n, int p, int c, int T, long long ntiles) {
@@ -162,20 +169,24 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
   // Stage buffer `b` holds A rows at smem + b*(BM+BN)*PITCH, then B rows.
   constexpr int kStage = (BM + BN) * PITCH;
 
-  float4 ra0[4], rb0[4], ra1[4], rb1[4];
-  const int nk = (c + BK - 1) / BK;
-  load_chunk<kVec4>(z, rows, c, row0, 0, ra0);
-  load_chunk<kVec4>(z, rows, c, col0, 0, rb0);
-  if (nk > 1) {
-    load_chunk<kVec4>(z, rows, c, row0, BK, ra1);
-    load_chunk<kVec4>(z, rows, c, col0, BK, rb1);
-  }
+  stage4 ra0[4], rb0[4], ra1[4], rb1[4];
+  // An even number of chunks, so the K loop below leaves only at its end: an exit
+  // between its two halves makes the compiler carry the accumulators in two register
+  // sets and copy all 64 of them every iteration.  A chunk past the channel count
+  // loads zeros and adds nothing (kLoad 2 requires c to be a multiple of two chunks).
+  // Prefetches and stores are unconditional, the prefetched chunk index clamped to
+  // the last chunk, so the loop body is straight-line code: the count of loads in
+  // flight is the same at every wait and the wait before each LDS store leaves the
+  // newer set in flight.
+  const int nk = ((c + BK - 1) / BK + 1) & ~1;
+  load_chunk<kLoad>(z, rows, c, row0, 0, ra0);
+  load_chunk<kLoad>(z, rows, c, col0, 0, rb0);
+  load_chunk<kLoad>(z, rows, c, row0, BK, ra1);
+  load_chunk<kLoad>(z, rows, c, col0, BK, rb1);
   store_chunk(smem, ra0);
   store_chunk(smem + BM * PITCH, rb0);
-  if (nk > 2) {
-    load_chunk<kVec4>(z, rows, c, row0, 2 * BK, ra0);
-    load_chunk<kVec4>(z, rows, c, col0, 2 * BK, rb0);
-  }
+  load_chunk<kLoad>(z, rows, c, row0, min(2, nk - 1) * BK, ra0);
+  load_chunk<kLoad>(z, rows, c, col0, min(2, nk - 1) * BK, rb0);
   __syncthreads();
 
   auto compute = [&](int buf) {
@@ -202,25 +213,18 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
   // iteration before it is consumed; loads run two compute phases ahead.
   for (int kc = 0; kc < nk; kc += 2) {
     compute(0);
-    if (kc + 1 < nk) {
-      store_chunk(smem + kStage, ra1);
-      store_chunk(smem + kStage + BM * PITCH, rb1);
-      if (kc + 3 < nk) {
-        load_chunk<kVec4>(z, rows, c, row0, (kc + 3) * BK, ra1);
-        load_chunk<kVec4>(z, rows, c, col0, (kc + 3) * BK, rb1);
-      }
-    }
+    store_chunk(smem + kStage, ra1);
+    store_chunk(smem + kStage + BM * PITCH, rb1);
+    load_chunk<kLoad>(z, rows, c, row0, min(kc + 3, nk - 1) * BK, ra1);
+    load_chunk<kLoad>(z, rows, c, col0, min(kc + 3, nk - 1) * BK, rb1);
     __syncthreads();
-    if (kc + 1 >= nk) break;
     compute(1);
-    if (kc + 2 < nk) {
-      store_chunk(smem, ra0);
-      store_chunk(smem + BM * PITCH, rb0);
-      if (kc + 4 < nk) {
-        load_chunk<kVec4>(z, rows, c, row0, (kc + 4) * BK, ra0);
-        load_chunk<kVec4>(z, rows, c, col0, (kc + 4) * BK, rb0);
-      }
-    }
+    // after the last compute this stores a clamped prefetch into buffer 0, which
+    // nothing reads any more (the epilogue reuses the buffers after two barriers)
+    store_chunk(smem, ra0);
+    store_chunk(smem + BM * PITCH, rb0);
+    load_chunk<kLoad>(z, rows, c, row0, min(kc + 4, nk - 1) * BK, ra0);
+    load_chunk<kLoad>(z, rows, c, col0, min(kc + 4, nk - 1) * BK, rb0);
     __syncthreads();
   }
 
@@ -542,10 +546,12 @@ inline int run_pairs(const float* z, int n, int p, int c, const Workspace& w, hi
   hipLaunchKernelGGL((msm_pair_min_kernel<V4, SPLIT>), dim3((unsigned)grid), dim3(THREADS), 0, s, z, w.norms, w.inv, \
                      w.minbits, (int)rows, n, p, c, (int)T, ntiles)
   const bool split = p >= BM;
-  if ((c & 3) == 0) {
-    if (split) MUSC_PAIR_LAUNCH(true, true); else MUSC_PAIR_LAUNCH(true, false);
+  if (c % (2 * BK) == 0) {
+    if (split) MUSC_PAIR_LAUNCH(2, true); else MUSC_PAIR_LAUNCH(2, false);
+  } else if ((c & 3) == 0) {
+    if (split) MUSC_PAIR_LAUNCH(1, true); else MUSC_PAIR_LAUNCH(1, false);
   } else {
-    if (split) MUSC_PAIR_LAUNCH(false, true); else MUSC_PAIR_LAUNCH(false, false);
+    if (split) MUSC_PAIR_LAUNCH(0, true); else MUSC_PAIR_LAUNCH(0, false);
   }
 #undef MUSC_PAIR_LAUNCH
   return check_launch();
