@@ -1,7 +1,10 @@
 // Calibration kernel: the sustained fp32 MFMA rate of this device with no memory
-// traffic in the loop (each wave issues independent v_mfma_f32_32x32x2f32 on four
+// traffic in the loop (each wave issues independent v_mfma_f32_32x32x2f32 on eight
 // accumulators back to back).  Used to state how far the hot kernels are from
-// what the part delivers under full MFMA load, next to the datasheet peak.
+// what the part delivers under full MFMA load, next to the datasheet peak.  Eight
+// chains, not four: with four per wave and every workgroup of the grid resident at
+// once (the kernel needs few registers) the loop measured 12 % below the rate that
+// one to four waves per SIMD reach with either chain count.
 #include "common.hpp"
 
 namespace musc {
@@ -10,37 +13,35 @@ namespace cal {
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 __global__ __launch_bounds__(256, 2) void mfma_f32_loop(float* __restrict__ out, int iters, float seed) {
-  floatx16 acc[4];
+  floatx16 acc[8];
 #pragma unroll
-  for (int b = 0; b < 4; ++b)
+  for (int b = 0; b < 8; ++b)
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[b][v] = 0.f;
   const float a = seed + threadIdx.x * 1e-3f, c = seed - threadIdx.x * 1e-3f;
   for (int i = 0; i < iters; ++i) {
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, c, acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(c, a, acc[1], 0, 0, 0);
-      acc[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, a, acc[2], 0, 0, 0);
-      acc[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(c, c, acc[3], 0, 0, 0);
-    }
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+      for (int b = 0; b < 8; ++b)   // 64 MFMAs per iteration
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32((b & 1) ? a : c, (b & 2) ? c : a, acc[b], 0, 0, 0);
   }
   float s = 0.f;
 #pragma unroll
-  for (int b = 0; b < 4; ++b)
+  for (int b = 0; b < 8; ++b)
 #pragma unroll
     for (int v = 0; v < 16; ++v) s += acc[b][v];
   out[(long long)blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
-// fp16 counterpart: independent v_mfma_f32_32x32x16_f16 on four accumulators (the
+// fp16 counterpart: independent v_mfma_f32_32x32x16_f16 on eight accumulators (the
 // instruction of the split MSM engine).
 typedef _Float16 cal_half8 __attribute__((ext_vector_type(8)));
 
 __global__ __launch_bounds__(256, 2) void mfma_f16_loop(float* __restrict__ out, int iters, float seed) {
-  floatx16 acc[4];
+  floatx16 acc[8];
 #pragma unroll
-  for (int b = 0; b < 4; ++b)
+  for (int b = 0; b < 8; ++b)
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[b][v] = 0.f;
   cal_half8 a, c;
@@ -51,16 +52,14 @@ __global__ __launch_bounds__(256, 2) void mfma_f16_loop(float* __restrict__ out,
   }
   for (int i = 0; i < iters; ++i) {
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, c, acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(c, a, acc[1], 0, 0, 0);
-      acc[2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, a, acc[2], 0, 0, 0);
-      acc[3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(c, c, acc[3], 0, 0, 0);
-    }
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+      for (int b = 0; b < 8; ++b)   // 64 MFMAs per iteration
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16((b & 1) ? a : c, (b & 2) ? c : a, acc[b], 0, 0, 0);
   }
   float s = 0.f;
 #pragma unroll
-  for (int b = 0; b < 4; ++b)
+  for (int b = 0; b < 8; ++b)
 #pragma unroll
     for (int v = 0; v < 16; ++v) s += acc[b][v];
   out[(long long)blockIdx.x * blockDim.x + threadIdx.x] = s;
