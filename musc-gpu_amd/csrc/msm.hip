@@ -246,8 +246,8 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
           const float cn = s_cnorm[wn * 64 + nb * 32 + lr];
           const float ci = s_cinv[wn * 64 + nb * 32 + lr];
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            d2[mb][nb][g * 4 + e] = fmaxf(fmaf(rs[e] * ci, acc[mb][nb][g * 4 + e], rv[e] + cn), 0.f);
+          for (int e = 0; e < 4; ++e)  // clamped at 0 after the minima: max(., 0) commutes with min
+            d2[mb][nb][g * 4 + e] = fmaf(rs[e] * ci, acc[mb][nb][g * 4 + e], rv[e] + cn);
         }
       }
     // column minima over this wave's 64 rows: in-lane, then across the two lane halves
@@ -279,8 +279,8 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
     __syncthreads();  // operand buffers are no longer read
     float* s_cmin = smem;             // [2 (wm)][BN]
     float* s_rmin = smem + 2 * BN;    // [2 (wn)][BM]
-    s_cmin[wm * BN + wn * 64 + lh * 32 + lr] = cmin[0];
-    s_rmin[wn * BM + wm * 64 + (lr >> 4) * 32 + ((lr & 15) >> 2) * 8 + lh * 4 + (lr & 3)] = rv[0];
+    s_cmin[wm * BN + wn * 64 + lh * 32 + lr] = fmaxf(cmin[0], 0.f);
+    s_rmin[wn * BM + wm * 64 + (lr >> 4) * 32 + ((lr & 15) >> 2) * 8 + lh * 4 + (lr & 3)] = fmaxf(rv[0], 0.f);
     __syncthreads();
     if (t < BM) {
       const float m = fminf(s_rmin[t], s_rmin[BM + t]);
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
           const int cimg = s_cimg[j];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float v = fmaxf(fmaf(rs[e] * ci, acc[mb][nb][g * 4 + e], rv[e] + cn), 0.f);
+            const float v = fmaf(rs[e] * ci, acc[mb][nb][g * 4 + e], rv[e] + cn);  // clamped after the minima
             const bool masked = rimg[e] == cimg || rimg[e] == n || cimg == n;
             d2[mb][nb][g * 4 + e] = masked ? inf : v;
           }
@@ -380,11 +380,11 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
     float* s_cminB = smem + 2 * BN;
     float* s_rminA = smem + 4 * BN;   // [2 (wn)][BM]
     float* s_rminB = smem + 4 * BN + 2 * BM;
-    s_cminA[wm * BN + wn * 64 + lh * 32 + lr] = cminA[0];
-    s_cminB[wm * BN + wn * 64 + lh * 32 + lr] = cminB[0];
+    s_cminA[wm * BN + wn * 64 + lh * 32 + lr] = fmaxf(cminA[0], 0.f);
+    s_cminB[wm * BN + wn * 64 + lh * 32 + lr] = fmaxf(cminB[0], 0.f);
     const int rk = wm * 64 + (lr >> 4) * 32 + ((lr & 15) >> 2) * 8 + lh * 4 + (lr & 3);
-    s_rminA[wn * BM + rk] = rowminA;
-    s_rminB[wn * BM + rk] = rowminB;
+    s_rminA[wn * BM + rk] = fmaxf(rowminA, 0.f);
+    s_rminB[wn * BM + rk] = fmaxf(rowminB, 0.f);
     __syncthreads();
     if (t < BM) {
       const int r = row0 + t;

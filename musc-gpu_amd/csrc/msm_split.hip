@@ -309,7 +309,8 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
         const int cimg = s_cimg[j];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float v = fmaxf(fmaf(rs[e] * ci, acc[mb][nb][g * 4 + e], rv[e] + cn), 0.f);
+          // clamped at 0 after the minima: max(., 0) commutes with min
+          const float v = fmaf(rs[e] * ci, acc[mb][nb][g * 4 + e], rv[e] + cn);
           const bool masked = !simple && (rimg[e] == cimg || rimg[e] == n || cimg == n);
           d2[mb][nb][g * 4 + e] = masked ? inf : v;
         }
@@ -349,8 +350,8 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
     float* s_cmin = reinterpret_cast<float*>(smem);  // [2 (wm)][TC]
     float* s_rmin = s_cmin + 2 * TC;                  // [2 (wn)][TR]
 #pragma unroll
-    for (int q = 0; q < 2; ++q) s_cmin[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = cm[q];
-    s_rmin[wn * TR + wm * 64 + transposed_row(lr, lh)] = rv[0];
+    for (int q = 0; q < 2; ++q) s_cmin[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = fmaxf(cm[q], 0.f);
+    s_rmin[wn * TR + wm * 64 + transposed_row(lr, lh)] = fmaxf(rv[0], 0.f);
     __syncthreads();
     atomicMin(minbits + (long long)(col0 + t) * n + rA, __float_as_uint(fminf(s_cmin[t], s_cmin[TC + t])));
     if (t < TR)
@@ -420,12 +421,12 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
   float* s_rminB = s_rminA + 2 * TR;
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    s_cminA[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = cmA[q];
-    s_cminB[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = cmB[q];
+    s_cminA[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = fmaxf(cmA[q], 0.f);
+    s_cminB[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = fmaxf(cmB[q], 0.f);
   }
   const int rk = wm * 64 + transposed_row(lr, lh);
-  s_rminA[wn * TR + rk] = rowminA;
-  s_rminB[wn * TR + rk] = rowminB;
+  s_rminA[wn * TR + rk] = fmaxf(rowminA, 0.f);
+  s_rminB[wn * TR + rk] = fmaxf(rowminB, 0.f);
   __syncthreads();
   {
     const int cc = col0 + t;
