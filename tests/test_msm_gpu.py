@@ -30,10 +30,11 @@ def test_golden(golden, device, case):
 # (p = 128: every tile inside one image; 129/130/200/257/300/1369: straddling tiles, padded
 # last tile row); p < 128 the LDS epilogue (several images per tile); c % 4 != 0 the masked loads;
 # c % 64 != 0 (36, 100, 7, 33, 4, 96, 32) the channel-masked loads, with an odd number of 32-channel
-# chunks rounded up by a zero chunk (7, 33, 4, 96, 32)
+# chunks rounded up by a zero chunk (7, 33, 4, 96, 32); c % 64 == 0 the unmasked whole-chunk loads,
+# with the register epilogues (1024, 64 at p >= 128) and with the LDS epilogue (128, 64 at p < 128)
 @pytest.mark.parametrize('n,p,c', [(5, 200, 36), (9, 130, 1024), (17, 64, 100), (6, 129, 7), (12, 257, 33),
                                    (40, 3, 4), (7, 128, 64), (5, 300, 1024), (5, 1369, 64), (8, 150, 96),
-                                   (6, 140, 32)])
+                                   (6, 140, 32), (30, 60, 128), (12, 100, 64)])
 def test_random_shapes_vs_oracles(device, n, p, c):
     torch.manual_seed(n * 1000 + p)
     z = torch.nn.functional.normalize(torch.randn((n, p, c)), dim=-1)
