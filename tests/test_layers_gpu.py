@@ -96,6 +96,34 @@ def test_quick_gelu_fp16_matches_torch_ops(device):
     assert (got == ref).float().mean() > 0.999
 
 
+def _all_finite_fp16(device):
+    bits = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16)
+    x = bits.view(torch.float16)
+    return x[torch.isfinite(x)].contiguous().to(device)    # 63488 values, both zeros, subnormals
+
+
+def test_quick_gelu_fp16_every_input(device):
+    # the activation is elementwise, so agreement on every finite fp16 value is agreement
+    # on any tensor: bit-identical to torch's three-op fp16 chain (transformer.py:32-35)
+    x = _all_finite_fp16(device)
+    ref = x * torch.sigmoid(1.702 * x)
+    got = _layers_hip.activation_(x.clone(), rt.ACT_QUICK_GELU)
+    assert torch.equal(torch.isfinite(got), torch.isfinite(ref))
+    fin = torch.isfinite(ref)
+    match = (got[fin] == ref[fin]).float().mean().item()
+    print(f'QuickGELU fp16: {match:.6f} of {int(fin.sum())} finite inputs bit-identical to torch', flush=True)
+    assert torch.equal(got[fin], ref[fin])
+
+
+def test_gelu_fp16_every_input(device):
+    x = _all_finite_fp16(device)
+    ref = F.gelu(x)
+    got = _layers_hip.activation_(x.clone(), rt.ACT_GELU)
+    assert torch.equal(torch.isfinite(got), torch.isfinite(ref))
+    fin = torch.isfinite(ref)
+    _assert_fp16_close(got[fin], ref[fin], x[fin].float().abs())
+
+
 @pytest.mark.parametrize('mode', [0, 1])
 def test_activation_fp32(device, mode):
     g = torch.Generator().manual_seed(15 + mode)
