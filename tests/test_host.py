@@ -88,3 +88,27 @@ def test_aggregation_predicate():
     stride2 = SimpleNamespace(r=3, patch_maker=SimpleNamespace(stride=2),
                               LNA=SimpleNamespace(output_dim=8, preprocessing_modules=[0, 0]))
     assert not _lnamd_hip.supported(stride2, feats)
+
+
+def test_patch_embedding_hook_predicate_and_cpu_fallback():
+    # conv1 (kernel == stride, no padding / dilation / groups) is what the encoding plugin
+    # turns into patches @ W^T; anything else, and any input the GEMM path does not take
+    # (here: a CPU tensor), keeps the module's own forward
+    from musc_hip import _encoder_hip
+    conv = torch.nn.Conv2d(3, 16, kernel_size=14, stride=14, bias=False)
+    assert _encoder_hip._patch_conv(conv)
+    assert _encoder_hip._patch_conv(torch.nn.Conv2d(3, 16, kernel_size=(7, 5), stride=(7, 5)))
+    for other in (torch.nn.Conv2d(3, 16, 14, stride=7), torch.nn.Conv2d(3, 16, 14, stride=14, padding=1),
+                  torch.nn.Conv2d(3, 16, 14, stride=14, dilation=2), torch.nn.Conv2d(4, 16, 14, stride=14, groups=2),
+                  torch.nn.Conv2d(3, 16, 3, stride=3, padding='valid'), torch.nn.Linear(3, 16), None):
+        assert not _encoder_hip._patch_conv(other)
+    calls = []
+
+    def original(x):
+        calls.append(x)
+        return conv._conv_forward(x, conv.weight, conv.bias)
+    hook = _encoder_hip._patch_embed_forward(conv, original)
+    x = torch.rand((1, 3, 28, 28))
+    with torch.no_grad():
+        out = hook(x)
+    assert len(calls) == 1 and out.shape == (1, 16, 2, 2)
