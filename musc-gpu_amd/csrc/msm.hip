@@ -36,6 +36,7 @@ constexpr int THREADS = 256;     // 4 waves, each owns a 64x64 sub-tile
 constexpr int kStageFloats = 2 * (BM + BN) * PITCH;       // double-buffered A and B
 constexpr int kEpiFloats = BM * EPITCH;
 constexpr int kSmemFloats = kStageFloats > kEpiFloats ? kStageFloats : kEpiFloats;
+constexpr int kBufferFlags = 0x00020000;  // buffer resource word 3 for raw byte-addressed loads
 
 // ---------------------------------------------------------------------------
 // Row norms.
@@ -69,23 +70,15 @@ __global__ __launch_bounds__(256) void msm_norms_kernel(const float* __restrict_
 // that the compiler left in scratch memory for the whole-chunk path.
 typedef float stage4 __attribute__((ext_vector_type(4)));
 
-// Operand loads: kLoad 2 = whole chunks (c a multiple of 2 * BK: no channel mask),
-// 1 = 16-byte loads with a channel mask (c % 4 == 0), 0 = scalar loads.
+// Channel-masked operand loads: kLoad 1 = 16-byte loads (c % 4 == 0), 0 = scalar loads.
+// (kLoad 2, whole chunks through a buffer resource, is in the kernel.)
 template <int kLoad>
 __device__ inline void load_chunk(const float* __restrict__ z, int rows, int c, int row0, int k0,
                                   stage4 (&reg)[4]) {
+  static_assert(kLoad == 0 || kLoad == 1, "whole-chunk loads are issued by the kernel");
   const int t = threadIdx.x;
   const int lrow = t / (BK / 4);
   const int lk = (t % (BK / 4)) * 4;
-  if constexpr (kLoad == 2) {
-    // padded rows re-read the last row (masked later)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = min(row0 + lrow + 32 * i, rows - 1);
-      reg[i] = *reinterpret_cast<const stage4*>(z + (long long)r * c + k0 + lk);
-    }
-    return;
-  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = row0 + lrow + 32 * i;
@@ -170,6 +163,32 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
   constexpr int kStage = (BM + BN) * PITCH;
 
   stage4 ra0[4], rb0[4], ra1[4], rb1[4];
+  // Whole-chunk loads (kLoad 2) go through a buffer resource over z: the byte offset of
+  // each staged row is computed once per tile and the chunk offset is the scalar offset,
+  // so the K loop does no address arithmetic (the host takes this path for pools under
+  // 2 GiB).  Padded rows re-read the last row (masked in the epilogue).
+  const __amdgpu_buffer_rsrc_t zr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(z), (short)0, (int)(uint32_t)((unsigned long long)rows * (unsigned long long)c * 4ull),
+      kBufferFlags);
+  uint32_t voffA[4], voffB[4];
+  if constexpr (kLoad == 2) {
+    const int lrow = t / (BK / 4), lk = (t % (BK / 4)) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      voffA[i] = ((uint32_t)min(row0 + lrow + 32 * i, rows - 1) * (uint32_t)c + (uint32_t)lk) * 4u;
+      voffB[i] = ((uint32_t)min(col0 + lrow + 32 * i, rows - 1) * (uint32_t)c + (uint32_t)lk) * 4u;
+    }
+  }
+  auto load = [&](bool rowsA, int k0, stage4 (&reg)[4]) {
+    if constexpr (kLoad == 2) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        reg[i] = __builtin_bit_cast(stage4, __builtin_amdgcn_raw_buffer_load_b128(zr, (int)(rowsA ? voffA[i] : voffB[i]),
+                                                                                  k0 * 4, 0));
+    } else {
+      load_chunk<kLoad>(z, rows, c, rowsA ? row0 : col0, k0, reg);
+    }
+  };
   // An even number of chunks, so the K loop below leaves only at its end: an exit
   // between its two halves makes the compiler carry the accumulators in two register
   // sets and copy all 64 of them every iteration.  A chunk past the channel count
@@ -179,14 +198,14 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
   // flight is the same at every wait and the wait before each LDS store leaves the
   // newer set in flight.
   const int nk = ((c + BK - 1) / BK + 1) & ~1;
-  load_chunk<kLoad>(z, rows, c, row0, 0, ra0);
-  load_chunk<kLoad>(z, rows, c, col0, 0, rb0);
-  load_chunk<kLoad>(z, rows, c, row0, BK, ra1);
-  load_chunk<kLoad>(z, rows, c, col0, BK, rb1);
+  load(true, 0, ra0);
+  load(false, 0, rb0);
+  load(true, BK, ra1);
+  load(false, BK, rb1);
   store_chunk(smem, ra0);
   store_chunk(smem + BM * PITCH, rb0);
-  load_chunk<kLoad>(z, rows, c, row0, min(2, nk - 1) * BK, ra0);
-  load_chunk<kLoad>(z, rows, c, col0, min(2, nk - 1) * BK, rb0);
+  load(true, min(2, nk - 1) * BK, ra0);
+  load(false, min(2, nk - 1) * BK, rb0);
   __syncthreads();
 
   auto compute = [&](int buf) {
@@ -215,16 +234,16 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
     compute(0);
     store_chunk(smem + kStage, ra1);
     store_chunk(smem + kStage + BM * PITCH, rb1);
-    load_chunk<kLoad>(z, rows, c, row0, min(kc + 3, nk - 1) * BK, ra1);
-    load_chunk<kLoad>(z, rows, c, col0, min(kc + 3, nk - 1) * BK, rb1);
+    load(true, min(kc + 3, nk - 1) * BK, ra1);
+    load(false, min(kc + 3, nk - 1) * BK, rb1);
     __syncthreads();
     compute(1);
     // after the last compute this stores a clamped prefetch into buffer 0, which
     // nothing reads any more (the epilogue reuses the buffers after two barriers)
     store_chunk(smem, ra0);
     store_chunk(smem + BM * PITCH, rb0);
-    load_chunk<kLoad>(z, rows, c, row0, min(kc + 4, nk - 1) * BK, ra0);
-    load_chunk<kLoad>(z, rows, c, col0, min(kc + 4, nk - 1) * BK, rb0);
+    load(true, min(kc + 4, nk - 1) * BK, ra0);
+    load(false, min(kc + 4, nk - 1) * BK, rb0);
     __syncthreads();
   }
 
@@ -546,7 +565,7 @@ inline int run_pairs(const float* z, int n, int p, int c, const Workspace& w, hi
   hipLaunchKernelGGL((msm_pair_min_kernel<V4, SPLIT>), dim3((unsigned)grid), dim3(THREADS), 0, s, z, w.norms, w.inv, \
                      w.minbits, (int)rows, n, p, c, (int)T, ntiles)
   const bool split = p >= BM;
-  if (c % (2 * BK) == 0) {
+  if (c % (2 * BK) == 0 && (unsigned long long)rows * (unsigned long long)c * 4ull < (1ull << 31)) {
     if (split) MUSC_PAIR_LAUNCH(2, true); else MUSC_PAIR_LAUNCH(2, false);
   } else if ((c & 3) == 0) {
     if (split) MUSC_PAIR_LAUNCH(1, true); else MUSC_PAIR_LAUNCH(1, false);
