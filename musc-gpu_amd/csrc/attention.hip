@@ -60,6 +60,8 @@ __device__ inline float halves_sum(float v) {
 // contiguous (batch*heads, t, 64) layout is sb = heads*t*64, sh = t*64, st = 64; the
 // packed in-projection output (t, batch, 3, heads, 64) of nn.MultiheadAttention is
 // read in place with st = batch*3*heads*64, sb = 3*heads*64, sh = 64.
+constexpr int kBufferFlags = 0x00020000;  // buffer resource word 3 for raw byte-addressed loads
+
 struct HeadLayout {
   long long sb, sh, st;
   int heads;
@@ -86,18 +88,6 @@ __device__ inline void st4(void* base, long long idx4, float4 v) {
     raw.y = *reinterpret_cast<uint32_t*>(&hi);
     reinterpret_cast<uint2*>(base)[idx4] = raw;
   }
-}
-
-// K / V^T staging: each thread loads two float4 of K and two of V per 32-key block
-// (idx = tid + 256*i -> key idx/16, channels 4*(idx%16)) into registers, one block
-// ahead of the compute; the LDS copy is double-buffered so one barrier per block
-// suffices.
-__device__ inline float4 load_kv_row(const float* __restrict__ src, long long head, long long st, int t, int kb,
-                                     int idx) {
-  const int key = idx / (D / 4), d4 = idx % (D / 4);
-  const int gk = kb * KB + key;
-  return gk < t ? *reinterpret_cast<const float4*>(src + head + (long long)gk * st + 4 * d4)
-                : make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
 __device__ inline void store_kv_row(float* __restrict__ Ks, float* __restrict__ Vt, int idx, float4 kv, float4 vv) {
@@ -149,19 +139,41 @@ __global__ __launch_bounds__(WAVES * kWave, 3) void attn_fwd_kernel(const float*
   const int nkb = (t + KB - 1) / KB;
   // K / V^T staging: thread tid moves elements idx = tid and tid + 256 of each
   // 32-key block (key idx/16, channels 4*(idx%16)), loaded one block ahead; the LDS
-  // copy is double-buffered, so one barrier per block suffices.
+  // copy is double-buffered, so one barrier per block suffices.  The loads go through
+  // a buffer resource based at the block's first key whose extent ends with the last
+  // valid key, so a key past t reads zeros and each thread's byte offset within the
+  // block is loop-invariant: no address arithmetic or bounds test per block.
   const int i0 = threadIdx.x, i1 = threadIdx.x + WAVES * kWave;
-  float4 k0 = load_kv_row(kg, head, st, t, 0, i0), k1 = load_kv_row(kg, head, st, t, 0, i1);
-  float4 v0 = load_kv_row(vg, head, st, t, 0, i0), v1 = load_kv_row(vg, head, st, t, 0, i1);
+  const uint32_t vo0 = (uint32_t)(((long long)(i0 / (D / 4)) * st + 4 * (i0 % (D / 4))) * 4);
+  const uint32_t vo1 = (uint32_t)(((long long)(i1 / (D / 4)) * st + 4 * (i1 % (D / 4))) * 4);
+  auto block_rsrc = [&](const float* src, int kb) {
+    const long long rem = min(t - kb * KB, KB);  // valid keys of the block, >= 1
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(src + head + (long long)kb * KB * st), (short)0,
+                                             (int)(((rem - 1) * st + D) * 4), kBufferFlags);
+  };
+  auto ldkv = [&](__amdgpu_buffer_rsrc_t r, uint32_t vo) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, 0, 0));
+  };
+  float4 k0, k1, v0, v1;
+  {
+    const __amdgpu_buffer_rsrc_t rk = block_rsrc(kg, 0), rv = block_rsrc(vg, 0);
+    k0 = ldkv(rk, vo0);
+    k1 = ldkv(rk, vo1);
+    v0 = ldkv(rv, vo0);
+    v1 = ldkv(rv, vo1);
+  }
   for (int kb = 0; kb < nkb; ++kb) {
     const int buf = kb & 1;
     store_kv_row(Ks[buf], Vt[buf], i0, k0, v0);
     store_kv_row(Ks[buf], Vt[buf], i1, k1, v1);
-    if (kb + 1 < nkb) {
-      k0 = load_kv_row(kg, head, st, t, kb + 1, i0);
-      k1 = load_kv_row(kg, head, st, t, kb + 1, i1);
-      v0 = load_kv_row(vg, head, st, t, kb + 1, i0);
-      v1 = load_kv_row(vg, head, st, t, kb + 1, i1);
+    {
+      // the block after the last is loaded again as the last block (never stored)
+      const int nb = min(kb + 1, nkb - 1);
+      const __amdgpu_buffer_rsrc_t rk = block_rsrc(kg, nb), rv = block_rsrc(vg, nb);
+      k0 = ldkv(rk, vo0);
+      k1 = ldkv(rk, vo1);
+      v0 = ldkv(rv, vo0);
+      v1 = ldkv(rv, vo1);
     }
     __syncthreads();
 
