@@ -306,17 +306,22 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
   // 2*(tid/16), 2*(tid/16)+1, halves 4*(tid%16).. (8 B each), one block ahead
   const int skey = tid / 8, sd8 = (tid % 8) * 8;
   const int kp = tid / 16, dg = tid % 16;
+  // loads through a buffer resource based at the block's first key whose extent ends
+  // with the last valid key: keys past t read zeros, offsets are loop-invariant
+  const uint32_t voK = (uint32_t)(((long long)skey * st + sd8) * 2);
+  const uint32_t voV0 = (uint32_t)(((long long)(2 * kp) * st + 4 * dg) * 2);
+  const uint32_t voV1 = (uint32_t)(((long long)(2 * kp + 1) * st + 4 * dg) * 2);
+  auto block_rsrc = [&](const _Float16* src, int kb) {
+    const long long rem = min(t - kb * KB, KB);  // valid keys of the block, >= 1
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(src + head + (long long)kb * KB * st), (short)0,
+                                             (int)(((rem - 1) * st + D) * 2), kBufferFlags);
+  };
   auto load_k = [&](int kb) -> half8 {
-    const int gk = kb * KB + skey;
-    half8 r = {};
-    if (gk < t) r = *reinterpret_cast<const half8*>(kg + head + (long long)gk * st + sd8);
-    return r;
+    return __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(block_rsrc(kg, kb), (int)voK, 0, 0));
   };
   auto load_v = [&](int kb, int which) -> half4 {
-    const int gk = kb * KB + 2 * kp + which;
-    half4 r = {};
-    if (gk < t) r = *reinterpret_cast<const half4*>(vg + head + (long long)gk * st + 4 * dg);
-    return r;
+    return __builtin_bit_cast(half4, __builtin_amdgcn_raw_buffer_load_b64(block_rsrc(vg, kb), (int)(which ? voV1 : voV0),
+                                                                           0, 0));
   };
   auto store_k = [&](int buf, half8 kr) { *reinterpret_cast<half8*>(&Ks[buf][skey * KP16 + sd8]) = kr; };
   auto store_v = [&](int buf, half4 a, half4 b) {
