@@ -68,63 +68,141 @@ def profiled_traffic(config: str):
     return None
 
 
-def cpu_baseline(tokens_cpu, pools_gpu, r_list, image_size, gpu_scores_rl0, budget_s: float = 12.0):
-    """Time the oracle (torch CPU restatement of the original backend) on a bounded sample.
+def host_cpus() -> dict:
+    """What this process may run on: logical CPUs, its affinity set, a cgroup CPU quota,
+    physical cores and the CPU model."""
+    info = {'os_cpu_count': os.cpu_count()}
+    try:
+        info['affinity_cpus'] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        info['affinity_cpus'] = os.cpu_count()
+    quota = None
+    try:
+        q, period = open('/sys/fs/cgroup/cpu.max').read().split()[:2]
+        if q != 'max':
+            quota = float(q) / float(period)
+    except (OSError, ValueError):
+        pass
+    info['cgroup_cpu_quota'] = quota
+    try:
+        import psutil
+        info['physical_cores'] = psutil.cpu_count(logical=False)
+    except Exception:
+        info['physical_cores'] = None
+    model = None
+    try:
+        for line in open('/proc/cpuinfo'):
+            if line.startswith('model name'):
+                model = line.split(':', 1)[1].strip()
+                break
+    except OSError:
+        pass
+    info['cpu_model'] = model
+    usable = info['affinity_cpus'] or 1
+    if quota is not None:
+        usable = max(1, min(usable, int(quota + 0.5)))
+    info['usable_cpus'] = usable
+    return info
 
-    Sample: LNAMD (Unfold path) for one batch of 4 images, every layer and radius;
-    compute_scores_fast for a few query images of one (radius, layer) pool; the
-    epilogue on the full score tensor.  Extrapolated to the whole job.
+
+def cpu_baseline(tokens_cpu, pools_gpu, scores_gpu, maps_gpu, r_list, image_size, reps: int = 3,
+                 queries_per_pool: int = 2):
+    """Time the oracle (torch CPU restatement of the original backend) on a bounded sample,
+    and check the GPU results it covers with the agreement gate.
+
+    Sample, repeated `reps` times (median reported): LNAMD (Unfold path) for one batch of 4
+    images, every layer and radius; compute_scores_fast for `queries_per_pool` query images
+    of every (radius, layer) pool (the GPU's own LNAMD output, normalised); the epilogue on
+    the GPU's full score tensor.  Extrapolated to the whole job.  The same outputs are
+    compared with the GPU's LNAMD features, score rows and maps (compare_arrays).
     """
+    import statistics
+
     import torch
+    from musc_hip import agreement
     from oracle import epilogue as oe
     from oracle import lnamd as ol
     from oracle import msm as om
 
-    threads = min(16, os.cpu_count() or 1)
+    cpus = host_cpus()
+    threads = cpus['usable_cpus']
     torch.set_num_threads(threads)
     n = tokens_cpu[0].shape[0]
     n_layers = len(tokens_cpu)
-    batch = 4
-    t0 = time.perf_counter()
-    with torch.no_grad():
-        for r in r_list:
-            f = ol.lnamd_embed([t[:batch] for t in tokens_cpu], r)
-            ol.l2_normalise(f)
-    t_lnamd_batch = time.perf_counter() - t0
-    z = pools_gpu[0, 0].cpu()
-    z = z / z.norm(dim=-1, keepdim=True)      # the pools hold unnormalised window sums
-    q_times, errs = [], []
-    # up to 48 query images spread over the pool, until the time budget is spent
-    queries = sorted(set(int(round(k * (n - 1) / 47)) for k in range(48)), key=lambda i: (i * 37) % n)
-    spent = 0.0
-    for i in queries:
-        t1 = time.perf_counter()
-        ref = om.compute_scores_fast(z, i).double()
-        dt = time.perf_counter() - t1
-        q_times.append(dt)
-        spent += dt
-        errs.append((ref - gpu_scores_rl0[i]).abs().max().item())
-        if spent > budget_s and len(q_times) >= 2:
-            break
-    t_query = sum(q_times) / len(q_times)
-    fake = [[torch.rand((n, z.shape[1]), dtype=torch.float64) for _ in range(n_layers)] for _ in r_list]
-    t2 = time.perf_counter()
-    oe.maps_and_scores(fake, image_size)
-    t_epi = time.perf_counter() - t2
-    n_batches = (n + batch - 1) // batch
-    total = n_batches * t_lnamd_batch + len(r_list) * n_layers * n * t_query + t_epi
+    n_r = len(r_list)
+    batch = min(4, n)
+    picks = {}
+    for ri in range(n_r):
+        for li in range(n_layers):
+            k = ri * n_layers + li
+            picks[(ri, li)] = [(k * 37 + q * 41 + 7) % n for q in range(queries_per_pool)]
+    zs = {}
+    for (ri, li) in picks:
+        z = pools_gpu[ri, li].cpu()
+        zs[(ri, li)] = z / z.norm(dim=-1, keepdim=True)   # the pools hold unnormalised window sums
+    scores_cpu = scores_gpu.cpu()
+    totals, lnamd_t, query_t, epi_t = [], [], [], []
+    gate = {}
+    for rep in range(reps):
+        t0 = time.perf_counter()
+        feats = []
+        with torch.no_grad():
+            for r in r_list:
+                feats.append(ol.l2_normalise(ol.lnamd_embed([t[:batch] for t in tokens_cpu], r)))
+        t_lnamd = time.perf_counter() - t0
+        rows_ref, rows_gpu, q_times = [], [], []
+        for (ri, li), imgs in picks.items():
+            for i in imgs:
+                t1 = time.perf_counter()
+                ref = om.compute_scores_fast(zs[(ri, li)], i).double()
+                q_times.append(time.perf_counter() - t1)
+                rows_ref.append(ref)
+                rows_gpu.append(scores_cpu[ri, li, i])
+        t2 = time.perf_counter()
+        ref_maps, ref_img = oe.maps_and_scores([[scores_cpu[ri, li] for li in range(n_layers)] for ri in range(n_r)],
+                                               image_size)
+        t_epi = time.perf_counter() - t2
+        t_query = statistics.median(q_times)
+        n_batches = (n + batch - 1) // batch
+        totals.append(n_batches * t_lnamd + n_r * n_layers * n * t_query + t_epi)
+        lnamd_t.append(t_lnamd)
+        query_t.append(t_query)
+        epi_t.append(t_epi)
+        if rep == 0:
+            gpu_feats = torch.stack([pools_gpu[ri, :, :batch].cpu() for ri in range(n_r)], 0)  # (R, L, b, P, C)
+            gpu_feats = gpu_feats / gpu_feats.norm(dim=-1, keepdim=True)
+            ref_feats = torch.stack([f.permute(2, 0, 1, 3) for f in feats], 0)               # (R, L, b, P, C)
+            rows = n_r * n_layers * batch                     # one gate row per (radius, layer, image)
+            gate['lnamd_features'] = agreement.compare_arrays(ref_feats.reshape(rows, -1),
+                                                              gpu_feats.reshape(rows, -1))
+            gate['msm_score_rows'] = agreement.compare_arrays(torch.stack(rows_ref, 0), torch.stack(rows_gpu, 0))
+            gate['maps'] = agreement.compare_arrays(ref_maps, maps_gpu.cpu())
+            gate['image_scores'] = agreement.compare_arrays(ref_img, maps_gpu.cpu().reshape(n, -1).max(-1)[0])
+            del gpu_feats, ref_feats
+        del feats
+    total = statistics.median(totals)
+    n_queries = sum(len(v) for v in picks.values())
+    gate['pass'] = all(g['pass'] for g in gate.values() if isinstance(g, dict))
     return {
         'value': n / total,
         'unit': 'images/s',
         'cores': threads,
         'kind': 'port',
-        'sample': (f'oracle torch-CPU restatement of the original backend: LNAMD Unfold path on {batch} images x '
-                   f'{n_layers} layers x radii {r_list} ({t_lnamd_batch:.2f} s), compute_scores_fast on '
-                   f'{len(q_times)} query images of one (radius, layer) pool ({t_query:.2f} s each), epilogue '
-                   f'({t_epi:.2f} s); extrapolated to {n_batches} LNAMD batches + '
-                   f'{len(r_list) * n_layers * n} query images'),
+        'host': cpus,
+        'torch_threads': torch.get_num_threads(),
+        'runs': reps,
+        'run_seconds_extrapolated': totals,
+        'sample': (f'oracle torch-CPU restatement of the original backend, median of {reps} runs: LNAMD Unfold path '
+                   f'on {batch} images x {n_layers} layers x radii {r_list} ({statistics.median(lnamd_t):.2f} s), '
+                   f'compute_scores_fast on {n_queries} query images spread over all {n_r * n_layers} (radius, '
+                   f'layer) pools ({statistics.median(query_t):.2f} s each), epilogue on the full score tensor '
+                   f'({statistics.median(epi_t):.2f} s); extrapolated to {(n + batch - 1) // batch} LNAMD batches + '
+                   f'{n_r * n_layers * n} query images'),
+        'extrapolated': True,
+        'sampled_fraction': {'lnamd_images': batch / n, 'msm_query_images': n_queries / (n_r * n_layers * n),
+                             'epilogue': 1.0},
         'extrapolated_seconds': total,
-        'sampled_query_max_abs_err_vs_gpu': max(errs),
+        'agreement': gate,
     }
 
 
@@ -145,13 +223,13 @@ def main() -> int:
         return 2
 
     import torch
-    from musc_hip import _MSM_hip, pipeline, synthetic
+    from musc_hip import _MSM_hip, agreement, pipeline, synthetic
     from musc_hip import _runtime as rt
 
     if not torch.cuda.is_available():
         print('bench.py needs a ROCm GPU', file=sys.stderr)
         return 2
-    ok, reason = rt.available()
+    ok, reason = rt.device_supported()
     if not ok:
         print(reason, file=sys.stderr)
         return 2
@@ -199,6 +277,10 @@ def main() -> int:
     del dev_tokens, pinned
 
     pair_ms = [a.elapsed_time(b) for a, b in timing['pairs']]
+    rank_ms = [a.elapsed_time(b) for a, b in timing['rank']]
+    rank_avg_s = sum(rank_ms) / len(rank_ms) / 1e3
+    rank_bytes = 4.0 * n * p * n + 8.0 * n * p        # minima keys read once, float64 scores written
+    rank_gbps = rank_bytes / rank_avg_s / 1e9
     lnamd_ms = [a.elapsed_time(b) for a, b in timing['lnamd']]
     pair_avg_s = sum(pair_ms) / len(pair_ms) / 1e3
     flop_per_launch = float(c) * p * p * n * (n - 1)
@@ -234,7 +316,12 @@ def main() -> int:
         'kernels': {'lnamd_all_radii': {'bound': 'hbm', 'achieved': lnamd_gbps, 'peak': HBM_PEAK_GBPS,
                                         'unit': 'GB/s', 'frac': lnamd_gbps / HBM_PEAK_GBPS,
                                         'algorithmic_bytes': lnamd_bytes, 'avg_launch_ms': lnamd_avg_s * 1e3,
-                                        'note': 'stats + finalize + stream kernels timed together'}},
+                                        'note': 'stats + finalize + stream kernels timed together'},
+                    'rank': {'bound': 'hbm', 'kernel': 'msm_rank_select_kernel', 'achieved': rank_gbps,
+                             'peak': HBM_PEAK_GBPS, 'unit': 'GB/s', 'frac': rank_gbps / HBM_PEAK_GBPS,
+                             'algorithmic_bytes': rank_bytes, 'avg_launch_ms': rank_avg_s * 1e3,
+                             'launches': len(rank_ms)}},
+        'agreement': {'evaluated': False},
         'cpu_baseline': None,
     }
     if not args.no_split and p >= _MSM_hip.SPLIT_MIN_P:
@@ -263,15 +350,30 @@ def main() -> int:
                          'note': 'three fp16 MFMA products per algorithmic fp32 dot product'},
             'max_abs_diff_maps_vs_fp32_engine': (maps16 - maps).abs().max().item(),
             'max_abs_diff_image_scores_vs_fp32_engine': (img16 - img).abs().max().item(),
+            'agreement_vs_fp32_engine': {'maps': agreement.compare_arrays(maps, maps16),
+                                         'image_scores': agreement.compare_arrays(img, img16)},
         }
+        sp = result['split16_engine']
+        if not all(g['pass'] for g in sp['agreement_vs_fp32_engine'].values()):
+            sp['value_withheld'] = sp.pop('value')
+            sp['value'] = None
+            sp['value_withheld_reason'] = 'split16 maps or image scores fail the 2e-5 agreement gate'
         log(f'[bench] split16 engine: {args.steps} steps in {sp_elapsed:.3f} s')
         del maps16, img16
     if not args.no_cpu_baseline:
-        log('[bench] timing the CPU baseline (oracle restatement, bounded sample)')
+        log('[bench] timing the CPU baseline (oracle restatement, bounded sample) and checking agreement')
         pools = pipeline.lnamd_pools(tokens, r_list)
-        scores = pipeline.msm_all(pools[:1, :1].contiguous())
+        scores = pipeline.msm_all(pools)
         torch.cuda.synchronize()
-        result['cpu_baseline'] = cpu_baseline(tokens_cpu, pools, r_list, image_size, scores[0, 0].cpu())
+        base = cpu_baseline(tokens_cpu, pools, scores, maps, r_list, image_size)
+        result['agreement'] = base.pop('agreement')
+        result['agreement']['evaluated'] = True
+        result['cpu_baseline'] = base
+        if not result['agreement']['pass']:
+            # the reference voids a speed claim whose results fail the gate (tools/benchmark.py:325-334)
+            result['value_withheld'] = result['value']
+            result['value'] = None
+            result['value_withheld_reason'] = 'GPU results fail the 2e-5 agreement gate against the oracle sample'
         log('[bench] CPU baseline done')
     print(json.dumps(result), flush=True)
     return 0

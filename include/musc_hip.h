@@ -46,6 +46,14 @@ const char* musc_strerror(int code);
 /* Library version, as MAJOR*10000 + MINOR*100 + PATCH. */
 int musc_version(void);
 
+/* The GPU architecture the kernels are compiled for ("gfx950").  A device whose
+ * architecture name (hipDeviceProp_t.gcnArchName up to the first ':') differs cannot
+ * run them; the backend selector then falls back to the original path, as the
+ * reference's selector does when its accelerated runtime cannot run
+ * (models/modules/_backend.py:10-13).  The reference's NVRTC bridge compiles for the
+ * device at first use instead (models/modules/_cuda_runtime.py:58-92). */
+const char* musc_target_arch(void);
+
 /* ------------------------------------------------------------------------ */
 /* Mutual scoring module (MSM).                                              */
 /* ------------------------------------------------------------------------ */

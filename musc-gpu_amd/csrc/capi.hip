@@ -14,3 +14,8 @@ extern "C" const char* musc_strerror(int code) {
 }
 
 extern "C" int musc_version(void) { return 100; }
+
+#ifndef MUSC_TARGET_ARCH
+#error "build with -DMUSC_TARGET_ARCH=\"<offload arch>\" (musc_hip/build.py passes it)"
+#endif
+extern "C" const char* musc_target_arch(void) { return MUSC_TARGET_ARCH; }

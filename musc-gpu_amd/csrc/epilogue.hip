@@ -10,7 +10,9 @@
 // n_layers score maps into LDS, then writes its kRows x S pixels (coalesced
 // float64 rows) and merges its band maximum into image_scores with a 64-bit
 // atomicMax on the bit pattern (all scores are non-negative distances, whose
-// IEEE bits order like the values).
+// IEEE bits order like the values).  The maximum propagates NaN, as numpy's max
+// at models/musc.py:288 does: NaN bit patterns (either sign) compare above every
+// non-negative number as unsigned integers, so the atomic keeps them too.
 #include "common.hpp"
 
 namespace musc {
@@ -20,6 +22,8 @@ constexpr int kRows = 8;
 constexpr int kThreads = 256;
 constexpr int kMaxSide = 128;
 constexpr int kMaxGridRows = 16;  // grid rows one band may touch
+
+__device__ inline double nmax(double a, double b) { return __builtin_elementwise_maximum(a, b); }
 
 __global__ __launch_bounds__(kThreads) void maps_kernel(const double* __restrict__ scores, int n_radii, int n_layers,
                                                         int n, int side, int out_size, double* __restrict__ maps,
@@ -64,18 +68,18 @@ __global__ __launch_bounds__(kThreads) void maps_kernel(const double* __restrict
     const double* r1 = avg[h1 - g0];
     const double v = lh0 * (lw0 * r0[w0] + lw1 * r0[w1]) + lh1 * (lw0 * r1[w0] + lw1 * r1[w1]);
     if (maps) maps[((long long)img * out_size + y) * out_size + x] = v;
-    vmax = fmax(vmax, v);
+    vmax = nmax(vmax, v);
   }
   if (image_bits) {
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) vmax = fmax(vmax, __shfl_xor(vmax, off, kWave));
+    for (int off = 32; off >= 1; off >>= 1) vmax = nmax(vmax, __shfl_xor(vmax, off, kWave));
     __shared__ double wmax[kThreads / kWave];
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     if (lane == 0) wmax[wave] = vmax;
     __syncthreads();
     if (threadIdx.x == 0) {
       double m = wmax[0];
-      for (int w = 1; w < (int)(blockDim.x / kWave); ++w) m = fmax(m, wmax[w]);
+      for (int w = 1; w < (int)(blockDim.x / kWave); ++w) m = nmax(m, wmax[w]);
       atomicMax(image_bits + img, (unsigned long long)__double_as_longlong(m));
     }
   }

@@ -15,12 +15,15 @@
 //                            ||a||^2 + ||b||^2 - 2 a.b (clamped at 0, as
 //                            torch.cdist's matmul path does), masks same-image
 //                            pairs, and reduces the tile along BOTH rows and
-//                            columns, segmented by image, merging the partial
-//                            minima with unsigned atomicMin on the float bits
-//                            (non-negative floats order like their bit patterns).
+//                            columns, segmented by image, with NaN-propagating
+//                            minima (as torch.min), merging the partial minima
+//                            with unsigned atomicMin on an order-preserving key
+//                            in which NaN wins (min_key, msm_common.hpp).
 //                            The distance matrix never reaches HBM.
-//   4. msm_rank_kernel       one wave per patch: rank the n-1 minima, average the
-//                            square roots of ranks [a, b).
+//   4. msm_rank_select_kernel  one thread per patch: the a-th and b-th smallest
+//                            of the n-1 minima (NaN last) by a binary search over
+//                            the key bits, then the mean of the square roots of
+//                            ranks [a, b).
 #include "msm_common.hpp"
 
 namespace musc {
@@ -277,14 +280,14 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) m = fminf(m, d2[mb][nb][v]);
+        for (int v = 0; v < 16; ++v) m = nmin(m, d2[mb][nb][v]);
       cmin[nb] = m;
     }
     {
       // half lh keeps column block nb = lh and receives the other half's value for it
       const float send = lh ? cmin[0] : cmin[1];
       const float keep = lh ? cmin[1] : cmin[0];
-      cmin[0] = fminf(keep, __shfl_xor(send, 32, kWave));
+      cmin[0] = nmin(keep, __shfl_xor(send, 32, kWave));
     }
     // row minima over this wave's 64 columns: min over nb in-lane, then a transposing
     // butterfly over the 32 lanes of each half (31 exchanges); lane lr ends with the
@@ -293,21 +296,19 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) rv[mb * 16 + v] = fminf(d2[mb][0][v], d2[mb][1][v]);
+      for (int v = 0; v < 16; ++v) rv[mb * 16 + v] = nmin(d2[mb][0][v], d2[mb][1][v]);
     transpose_min32(rv, lr);
     __syncthreads();  // operand buffers are no longer read
     float* s_cmin = smem;             // [2 (wm)][BN]
     float* s_rmin = smem + 2 * BN;    // [2 (wn)][BM]
-    s_cmin[wm * BN + wn * 64 + lh * 32 + lr] = fmaxf(cmin[0], 0.f);
-    s_rmin[wn * BM + wm * 64 + (lr >> 4) * 32 + ((lr & 15) >> 2) * 8 + lh * 4 + (lr & 3)] = fmaxf(rv[0], 0.f);
+    s_cmin[wm * BN + wn * 64 + lh * 32 + lr] = cmin[0];
+    s_rmin[wn * BM + wm * 64 + (lr >> 4) * 32 + ((lr & 15) >> 2) * 8 + lh * 4 + (lr & 3)] = rv[0];
     __syncthreads();
     if (t < BM) {
-      const float m = fminf(s_rmin[t], s_rmin[BM + t]);
-      atomicMin(minbits + (long long)(row0 + t) * n + cimg0, __float_as_uint(m));
+      atomicMin(minbits + (long long)(row0 + t) * n + cimg0, min_key(nmin(s_rmin[t], s_rmin[BM + t])));
     } else {
       const int j = t - BM;
-      const float m = fminf(s_cmin[j], s_cmin[BN + j]);
-      atomicMin(minbits + (long long)(col0 + j) * n + rimg0, __float_as_uint(m));
+      atomicMin(minbits + (long long)(col0 + j) * n + rimg0, min_key(nmin(s_cmin[j], s_cmin[BN + j])));
     }
     return;
   }
@@ -358,8 +359,8 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const float x = d2[mb][nb][v];
-          a = rowB[mb][v] ? a : fminf(a, x);
-          b = rowB[mb][v] ? fminf(b, x) : b;
+          a = rowB[mb][v] ? a : nmin(a, x);
+          b = rowB[mb][v] ? nmin(b, x) : b;
         }
       cminA[nb] = a;
       cminB[nb] = b;
@@ -367,8 +368,8 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
     {
       const float sendA = lh ? cminA[0] : cminA[1], keepA = lh ? cminA[1] : cminA[0];
       const float sendB = lh ? cminB[0] : cminB[1], keepB = lh ? cminB[1] : cminB[0];
-      cminA[0] = fminf(keepA, __shfl_xor(sendA, 32, kWave));
-      cminB[0] = fminf(keepB, __shfl_xor(sendB, 32, kWave));
+      cminA[0] = nmin(keepA, __shfl_xor(sendA, 32, kWave));
+      cminB[0] = nmin(keepB, __shfl_xor(sendB, 32, kWave));
     }
     // row minima over this wave's 64 columns, per column segment: transposing
     // butterflies as in the single-segment path, one per segment
@@ -380,7 +381,7 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int v = 0; v < 16; ++v)
-          rv[mb * 16 + v] = fminf(colB0 ? inf : d2[mb][0][v], colB1 ? inf : d2[mb][1][v]);
+          rv[mb * 16 + v] = nmin(colB0 ? inf : d2[mb][0][v], colB1 ? inf : d2[mb][1][v]);
       transpose_min32(rv, lr);
       rowminA = rv[0];
     }
@@ -390,7 +391,7 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int v = 0; v < 16; ++v)
-          rv[mb * 16 + v] = fminf(colB0 ? d2[mb][0][v] : inf, colB1 ? d2[mb][1][v] : inf);
+          rv[mb * 16 + v] = nmin(colB0 ? d2[mb][0][v] : inf, colB1 ? d2[mb][1][v] : inf);
       transpose_min32(rv, lr);
       rowminB = rv[0];
     }
@@ -399,28 +400,30 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
     float* s_cminB = smem + 2 * BN;
     float* s_rminA = smem + 4 * BN;   // [2 (wn)][BM]
     float* s_rminB = smem + 4 * BN + 2 * BM;
-    s_cminA[wm * BN + wn * 64 + lh * 32 + lr] = fmaxf(cminA[0], 0.f);
-    s_cminB[wm * BN + wn * 64 + lh * 32 + lr] = fmaxf(cminB[0], 0.f);
+    s_cminA[wm * BN + wn * 64 + lh * 32 + lr] = cminA[0];
+    s_cminB[wm * BN + wn * 64 + lh * 32 + lr] = cminB[0];
     const int rk = wm * 64 + (lr >> 4) * 32 + ((lr & 15) >> 2) * 8 + lh * 4 + (lr & 3);
-    s_rminA[wn * BM + rk] = fmaxf(rowminA, 0.f);
-    s_rminB[wn * BM + rk] = fmaxf(rowminB, 0.f);
+    s_rminA[wn * BM + rk] = rowminA;
+    s_rminB[wn * BM + rk] = rowminB;
     __syncthreads();
     if (t < BM) {
       const int r = row0 + t;
       if (r < rows) {
-        const float a = fminf(s_rminA[t], s_rminA[BM + t]);
-        const float b = fminf(s_rminB[t], s_rminB[BM + t]);
-        if (a < inf) atomicMin(minbits + (long long)r * n + cA, __float_as_uint(a));
-        if (b < inf) atomicMin(minbits + (long long)r * n + cA + 1, __float_as_uint(b));
+        // a segment with no pair of different images is exactly +inf (masked): skip
+        // it, also because segment B may be the padding image n
+        const float a = nmin(s_rminA[t], s_rminA[BM + t]);
+        const float b = nmin(s_rminB[t], s_rminB[BM + t]);
+        if (a != inf) atomicMin(minbits + (long long)r * n + cA, min_key(a));
+        if (b != inf) atomicMin(minbits + (long long)r * n + cA + 1, min_key(b));
       }
     } else {
       const int j = t - BM;
       const int cc = col0 + j;
       if (cc < rows) {
-        const float a = fminf(s_cminA[j], s_cminA[BN + j]);
-        const float b = fminf(s_cminB[j], s_cminB[BN + j]);
-        if (a < inf) atomicMin(minbits + (long long)cc * n + rA, __float_as_uint(a));
-        if (b < inf) atomicMin(minbits + (long long)cc * n + rA + 1, __float_as_uint(b));
+        const float a = nmin(s_cminA[j], s_cminA[BN + j]);
+        const float b = nmin(s_cminB[j], s_cminB[BN + j]);
+        if (a != inf) atomicMin(minbits + (long long)cc * n + rA, min_key(a));
+        if (b != inf) atomicMin(minbits + (long long)cc * n + rA + 1, min_key(b));
       }
     }
     return;
@@ -438,8 +441,7 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int i = wm * 64 + mb * 32 + (v >> 2) * 8 + lh * 4 + (v & 3);
-        float d2 = fmaf(cs * s_rinv[i], acc[mb][nb][v], s_rnorm[i] + cn);
-        d2 = fmaxf(d2, 0.f);
+        const float d2 = fmaf(cs * s_rinv[i], acc[mb][nb][v], s_rnorm[i] + cn);  // clamped by min_key
         const int ri = s_rimg[i];
         E[i * EPITCH + j] = (ri == ci || ri == n || ci == n) ? __int_as_float(kInfBits) : d2;
       }
@@ -456,13 +458,13 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
       for (int j = 0; j < BN; ++j) {
         const int ci = s_cimg[j];
         if (ci != seg) {
-          if (seg < n && cur < __int_as_float(kInfBits)) atomicMin(dst + seg, __float_as_uint(cur));
+          if (seg < n && cur != __int_as_float(kInfBits)) atomicMin(dst + seg, min_key(cur));
           seg = ci;
           cur = __int_as_float(kInfBits);
         }
-        cur = fminf(cur, E[t * EPITCH + j]);
+        cur = nmin(cur, E[t * EPITCH + j]);
       }
-      if (seg < n && cur < __int_as_float(kInfBits)) atomicMin(dst + seg, __float_as_uint(cur));
+      if (seg < n && cur != __int_as_float(kInfBits)) atomicMin(dst + seg, min_key(cur));
     }
   } else {
     // Column pass: the same tile seen from the reference side (symmetric reuse).
@@ -475,51 +477,117 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
       for (int i = 0; i < BM; ++i) {
         const int ri = s_rimg[i];
         if (ri != seg) {
-          if (seg < n && cur < __int_as_float(kInfBits)) atomicMin(dst + seg, __float_as_uint(cur));
+          if (seg < n && cur != __int_as_float(kInfBits)) atomicMin(dst + seg, min_key(cur));
           seg = ri;
           cur = __int_as_float(kInfBits);
         }
-        cur = fminf(cur, E[i * EPITCH + j]);
+        cur = nmin(cur, E[i * EPITCH + j]);
       }
-      if (seg < n && cur < __int_as_float(kInfBits)) atomicMin(dst + seg, __float_as_uint(cur));
+      if (seg < n && cur != __int_as_float(kInfBits)) atomicMin(dst + seg, min_key(cur));
     }
   }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Trimmed rank mean.  One wave per query patch; the n minima are staged in LDS
-// and every value's rank is counted (ties broken by image index), so the sum of
-// ranks [a, b) is exact for any multiset.
+// Trimmed rank means.  A row's minima keys (own image excluded) are ranked in
+// ascending order, NaN last (torch.topk(largest=False) of models/modules/_MSM.py:27
+// ranks NaN after every number).  The score is (S(b) - S(a)) / (b - a), S(k) being
+// the sum of the square roots of the k smallest minima (fp64), rounded to fp32 like
+// the reference's fp32 mean and widened (:30, :57).  With t the k-th smallest key,
+//   S(k) = sum_{key < t} sqrt(key) + (k - #{key < t}) * sqrt(t),
+// which holds for any ties; a NaN among the k smallest makes t = 0xffffffff (the NaN
+// key) and S(k) NaN, as the reference's mean over a window holding a NaN.
 // ---------------------------------------------------------------------------
+constexpr uint32_t kNoKey = 0xffffffffu;  // NaN minimum, own image, or padding
+
+// One thread per row, its n keys in registers (n <= kKeys).  t is found by a binary
+// search over the key bits: the largest t with #{key < t} < k, built from the most
+// significant bit down (32 steps of one compare and one add per key).  Rows sit
+// n * 4 bytes apart, so the loads of a wave cover one contiguous range.
+template <int kKeys>
+__global__ __launch_bounds__(64) void msm_rank_select_kernel(const uint32_t* __restrict__ minbits, int rows, int n,
+                                                             int p, int a, int b, double* __restrict__ scores) {
+  const long long row = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= rows) return;
+  const int self = (int)(row / p);
+  const uint32_t* src = minbits + row * n;
+  uint32_t key[kKeys];
+#pragma unroll
+  for (int j = 0; j < kKeys; ++j) key[j] = (j < n && j != self) ? key_bits(src[j]) : kNoKey;
+  uint32_t ta = 0, tb = 0;  // a-th and b-th smallest keys (ta stays 0 for a = 0)
+  if (a == 0) {
+#pragma unroll 1
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t cb = tb | (1u << bit);
+      int nb = 0;
+#pragma unroll
+      for (int j = 0; j < kKeys; ++j) nb += key[j] < cb;
+      tb = nb < b ? cb : tb;
+    }
+  } else {
+#pragma unroll 1
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t ca = ta | (1u << bit), cb = tb | (1u << bit);
+      int na = 0, nb = 0;
+#pragma unroll
+      for (int j = 0; j < kKeys; ++j) {
+        na += key[j] < ca;
+        nb += key[j] < cb;
+      }
+      ta = na < a ? ca : ta;
+      tb = nb < b ? cb : tb;
+    }
+  }
+  double sa = 0.0, sb = 0.0;
+  int la = 0, lb = 0;
+#pragma unroll
+  for (int j = 0; j < kKeys; ++j) {
+    const double r = (double)sqrtf(__uint_as_float(key[j]));
+    if (key[j] < tb) {
+      sb += r;
+      ++lb;
+    }
+    if (key[j] < ta) {
+      sa += r;
+      ++la;
+    }
+  }
+  sb += (double)(b - lb) * (double)sqrtf(__uint_as_float(tb));
+  if (a > 0) sa += (double)(a - la) * (double)sqrtf(__uint_as_float(ta));
+  scores[row] = (double)(float)((sb - sa) / (double)(b - a));
+}
+
+// Rows of more than 192 images: one wave per row, the n keys staged in LDS and each
+// key's rank counted (ties broken by image index).
 constexpr int kRankWaves = 4;
+constexpr int kMaxSelectKeys = 192;
 
 __global__ __launch_bounds__(kRankWaves * kWave) void msm_rank_kernel(
     const uint32_t* __restrict__ minbits, int rows, int n, int p, int a, int b,
     double* __restrict__ scores) {
-  extern __shared__ float s_vals[];  // kRankWaves * n
+  extern __shared__ uint32_t s_keys[];  // kRankWaves * n
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const long long row = (long long)blockIdx.x * kRankWaves + wave;
-  float* vals = s_vals + wave * n;
+  uint32_t* keys = s_keys + wave * n;
   const bool active = row < rows;
   const int self = active ? (int)(row / p) : -1;
   if (active) {
-    for (int j = lane; j < n; j += kWave)
-      vals[j] = j == self ? __int_as_float(kInfBits) : __uint_as_float(minbits[row * n + j]);
+    for (int j = lane; j < n; j += kWave) keys[j] = j == self ? kNoKey : key_bits(minbits[row * n + j]);
   }
   __syncthreads();
   if (!active) return;
   double sum = 0.0;
   for (int j = lane; j < n; j += kWave) {
     if (j == self) continue;
-    const float v = vals[j];
+    const uint32_t v = keys[j];
     int rank = 0;
     for (int k = 0; k < n; ++k) {
       if (k == self) continue;
-      const float u = vals[k];
+      const uint32_t u = keys[k];
       rank += (u < v) || (u == v && k < j);
     }
-    if (rank >= a && rank < b) sum += (double)sqrtf(v);
+    if (rank >= a && rank < b) sum += (double)sqrtf(__uint_as_float(v));
   }
   sum = wave_sum(sum);
   if (lane == 0) scores[row] = (double)(float)(sum / (double)(b - a));
@@ -532,7 +600,7 @@ __global__ __launch_bounds__(256) void msm_nearest_kernel(const uint32_t* __rest
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
     const size_t row = i / n;
     const int j = (int)(i % n);
-    nearest[i] = (j == (int)(row / p)) ? __int_as_float(kInfBits) : sqrtf(__uint_as_float(minbits[i]));
+    nearest[i] = (j == (int)(row / p)) ? __int_as_float(kInfBits) : sqrtf(__uint_as_float(key_bits(minbits[i])));
   }
 }
 
@@ -551,7 +619,7 @@ inline void run_prepare(const float* z, int n, int p, int c, int normalize, cons
   const long long rows = (long long)n * p;
   hipLaunchKernelGGL(msm_norms_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, z, (int)rows, c,
                      normalize, w.norms, w.inv);
-  launch_fill_u32(w.minbits, (size_t)rows * n, kInfBits, s);
+  launch_fill_u32(w.minbits, (size_t)rows * n, kMinFill, s);
 }
 
 // Stage 2: the fp32 MFMA pairwise-minima kernel (leaves squared minima bits).
@@ -579,7 +647,20 @@ inline int run_pairs(const float* z, int n, int p, int c, const Workspace& w, hi
 // Stage 3: trimmed rank means.
 int run_rank(int n, int p, int a, int b, double* scores, const Workspace& w, hipStream_t s) {
   const long long rows = (long long)n * p;
-  const size_t smem = (size_t)kRankWaves * n * sizeof(float);
+  if (n <= kMaxSelectKeys) {
+    const dim3 grid((unsigned)((rows + 63) / 64)), block(64);
+#define MUSC_RANK_LAUNCH(K) \
+  hipLaunchKernelGGL(msm_rank_select_kernel<K>, grid, block, 0, s, w.minbits, (int)rows, n, p, a, b, scores)
+    if (n <= 32) MUSC_RANK_LAUNCH(32);
+    else if (n <= 64) MUSC_RANK_LAUNCH(64);
+    else if (n <= 96) MUSC_RANK_LAUNCH(96);
+    else if (n <= 128) MUSC_RANK_LAUNCH(128);
+    else if (n <= 160) MUSC_RANK_LAUNCH(160);
+    else MUSC_RANK_LAUNCH(192);
+#undef MUSC_RANK_LAUNCH
+    return check_launch();
+  }
+  const size_t smem = (size_t)kRankWaves * n * sizeof(uint32_t);
   hipLaunchKernelGGL(msm_rank_kernel, dim3((unsigned)((rows + kRankWaves - 1) / kRankWaves)),
                      dim3(kRankWaves * kWave), smem, s, w.minbits, (int)rows, n, p, a, b, scores);
   return check_launch();

@@ -17,6 +17,34 @@ constexpr int BAND = 8;  // tile rows per band of the tile enumeration
 constexpr uint32_t kInfBits = 0x7f800000u;
 
 // ---------------------------------------------------------------------------
+// NaN semantics.  The reference's minima come from torch.min over cdist rows
+// (models/modules/_MSM.py:16-17), which propagates NaN: a patch whose distance to
+// any patch of image j is NaN (a row with a NaN, a zero row that the 0/0 of
+// models/musc.py:238 turned into NaN, the inf - inf of the expanded form) has a
+// NaN minimum for j.  So the epilogues reduce with the IEEE-754-2019 `minimum`
+// (v_minimum3_f32 on gfx950: one instruction, like fminf), never with fminf,
+// which drops NaN.
+//
+// The per-(row, image) minima are merged across tiles with an unsigned atomicMin
+// on a key in which NaN orders first: key(x) = 0 for NaN, else bits(max(x, 0)) + 1
+// (non-negative floats order like their bits; the +1 makes room for NaN; the
+// clamp at 0 is torch.cdist's clamp_min(0) of the squared distance, applied once
+// to the tile minimum since max(., 0) commutes with min).  The fill value is
+// key(+inf).  Readers subtract 1: NaN becomes 0xffffffff, which orders after
+// every number (torch.topk ranks NaN last, _MSM.py:27).
+// ---------------------------------------------------------------------------
+constexpr uint32_t kMinFill = kInfBits + 1u;  // key(+inf): "no pair seen yet"
+
+__device__ inline float nmin(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+
+__device__ inline uint32_t min_key(float x) {
+  return x > 0.f ? __float_as_uint(x) + 1u : (x == x ? 1u : 0u);
+}
+
+// key - 1: the squared distance's bits, 0xffffffff for NaN.
+__device__ inline uint32_t key_bits(uint32_t key) { return key - 1u; }
+
+// ---------------------------------------------------------------------------
 // Tile enumeration.  Tiles (I, J), I <= J < T, are numbered band by band (BAND
 // tile rows per band); inside a band the triangle (J < I0 + h) comes first,
 // then the rectangle in column-major order, so that the workgroups one XCD runs
@@ -96,7 +124,7 @@ __device__ inline float transpose_min32(float (&rv)[32], int lr) {
     for (int q = 0; q < half; ++q) {
       const float send = up ? rv[q] : rv[q + half];
       const float keep = up ? rv[q + half] : rv[q];
-      rv[q] = fminf(keep, butterfly_partner<half>(send));
+      rv[q] = nmin(keep, butterfly_partner<half>(send));
     }
   };
   stage(std::integral_constant<int, 16>{});
@@ -113,7 +141,8 @@ __device__ inline int transposed_row(int lr, int lh) {
   return (lr >> 4) * 32 + ((lr & 15) >> 2) * 8 + lh * 4 + (lr & 3);
 }
 
-// Workspace: norms (n*p fp32) | row scales (n*p fp32) | minima bits (n*p x n uint32).
+// Workspace: norms (n*p fp32) | row scales (n*p fp32) | minima keys (n*p x n uint32,
+// see min_key).
 struct Workspace {
   float* norms;
   float* inv;

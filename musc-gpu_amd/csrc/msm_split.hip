@@ -2,8 +2,12 @@
 //
 // Same contract as msm_pair_min_kernel (msm.hip), i.e. models/modules/_MSM.py:10-30:
 // per (patch, other image) the minimum squared distance ||a||^2 + ||b||^2 - 2 a.b,
-// clamped at 0, merged with atomicMin on the float bits; the trimmed rank means are
-// shared with the fp32 engine.  Only the dot products are formed differently.
+// clamped at 0, NaN-propagating, merged with atomicMin on min_key (msm_common.hpp);
+// the trimmed rank means are shared with the fp32 engine.  Only the dot products are
+// formed differently.  One difference at the edge: a row holding +-inf (possible only
+// without row normalisation; models/musc.py:238 turns such a row into NaN) has NaN
+// distances to every row here, where the expanded form of the fp32 engine and of
+// torch.cdist gives +inf for the pairs in which the infinite term adds to +inf.
 //
 // Split (Ootomo & Yokota, "Recovering single precision accuracy from Tensor Cores
 // while surpassing the FP32 theoretical peak performance", IJHPCA 2022, restated for
@@ -309,7 +313,7 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
         const int cimg = s_cimg[j];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          // clamped at 0 after the minima: max(., 0) commutes with min
+          // clamped at 0 by min_key, after the minima: max(., 0) commutes with min
           const float v = fmaf(rs[e] * ci, acc[mb][nb][g * 4 + e], rv[e] + cn);
           const bool masked = !simple && (rimg[e] == cimg || rimg[e] == n || cimg == n);
           d2[mb][nb][g * 4 + e] = masked ? inf : v;
@@ -327,7 +331,7 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) m = fminf(m, d2[mb][nb][v]);
+        for (int v = 0; v < 16; ++v) m = nmin(m, d2[mb][nb][v]);
       cmin[nb] = m;
     }
     float cm[2];
@@ -335,7 +339,7 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
     for (int q = 0; q < 2; ++q) {
       const float send = lh ? cmin[2 * q] : cmin[2 * q + 1];
       const float keep = lh ? cmin[2 * q + 1] : cmin[2 * q];
-      cm[q] = fminf(keep, __shfl_xor(send, 32, kWave));
+      cm[q] = nmin(keep, __shfl_xor(send, 32, kWave));
     }
     // row minima over this wave's 128 columns: in-lane over nb, then the transposing
     // butterfly over the 32 lanes of each half
@@ -344,18 +348,18 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int v = 0; v < 16; ++v)
-        rv[mb * 16 + v] = fminf(fminf(d2[mb][0][v], d2[mb][1][v]), fminf(d2[mb][2][v], d2[mb][3][v]));
+        rv[mb * 16 + v] = nmin(nmin(d2[mb][0][v], d2[mb][1][v]), nmin(d2[mb][2][v], d2[mb][3][v]));
     transpose_min32(rv, lr);
     __syncthreads();  // operand buffers are no longer read
     float* s_cmin = reinterpret_cast<float*>(smem);  // [2 (wm)][TC]
     float* s_rmin = s_cmin + 2 * TC;                  // [2 (wn)][TR]
 #pragma unroll
-    for (int q = 0; q < 2; ++q) s_cmin[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = fmaxf(cm[q], 0.f);
-    s_rmin[wn * TR + wm * 64 + transposed_row(lr, lh)] = fmaxf(rv[0], 0.f);
+    for (int q = 0; q < 2; ++q) s_cmin[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = cm[q];
+    s_rmin[wn * TR + wm * 64 + transposed_row(lr, lh)] = rv[0];
     __syncthreads();
-    atomicMin(minbits + (long long)(col0 + t) * n + rA, __float_as_uint(fminf(s_cmin[t], s_cmin[TC + t])));
+    atomicMin(minbits + (long long)(col0 + t) * n + rA, min_key(nmin(s_cmin[t], s_cmin[TC + t])));
     if (t < TR)
-      atomicMin(minbits + (long long)(row0 + t) * n + cA, __float_as_uint(fminf(s_rmin[t], s_rmin[TR + t])));
+      atomicMin(minbits + (long long)(row0 + t) * n + cA, min_key(nmin(s_rmin[t], s_rmin[TR + t])));
     return;
   }
 
@@ -370,8 +374,8 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const float x = d2[mb][nb][v];
-        a = rowB[mb][v] ? a : fminf(a, x);
-        b = rowB[mb][v] ? fminf(b, x) : b;
+        a = rowB[mb][v] ? a : nmin(a, x);
+        b = rowB[mb][v] ? nmin(b, x) : b;
       }
     cminA[nb] = a;
     cminB[nb] = b;
@@ -381,8 +385,8 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
   for (int q = 0; q < 2; ++q) {
     const float sendA = lh ? cminA[2 * q] : cminA[2 * q + 1], keepA = lh ? cminA[2 * q + 1] : cminA[2 * q];
     const float sendB = lh ? cminB[2 * q] : cminB[2 * q + 1], keepB = lh ? cminB[2 * q + 1] : cminB[2 * q];
-    cmA[q] = fminf(keepA, __shfl_xor(sendA, 32, kWave));
-    cmB[q] = fminf(keepB, __shfl_xor(sendB, 32, kWave));
+    cmA[q] = nmin(keepA, __shfl_xor(sendA, 32, kWave));
+    cmB[q] = nmin(keepB, __shfl_xor(sendB, 32, kWave));
   }
   bool colB[4];
 #pragma unroll
@@ -396,7 +400,7 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
       for (int v = 0; v < 16; ++v) {
         float m = inf;
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) m = fminf(m, colB[nb] ? inf : d2[mb][nb][v]);
+        for (int nb = 0; nb < 4; ++nb) m = nmin(m, colB[nb] ? inf : d2[mb][nb][v]);
         rv[mb * 16 + v] = m;
       }
     rowminA = transpose_min32(rv, lr);
@@ -409,7 +413,7 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
       for (int v = 0; v < 16; ++v) {
         float m = inf;
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) m = fminf(m, colB[nb] ? d2[mb][nb][v] : inf);
+        for (int nb = 0; nb < 4; ++nb) m = nmin(m, colB[nb] ? d2[mb][nb][v] : inf);
         rv[mb * 16 + v] = m;
       }
     rowminB = transpose_min32(rv, lr);
@@ -421,29 +425,31 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
   float* s_rminB = s_rminA + 2 * TR;
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    s_cminA[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = fmaxf(cmA[q], 0.f);
-    s_cminB[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = fmaxf(cmB[q], 0.f);
+    s_cminA[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = cmA[q];
+    s_cminB[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = cmB[q];
   }
   const int rk = wm * 64 + transposed_row(lr, lh);
-  s_rminA[wn * TR + rk] = fmaxf(rowminA, 0.f);
-  s_rminB[wn * TR + rk] = fmaxf(rowminB, 0.f);
+  s_rminA[wn * TR + rk] = rowminA;
+  s_rminB[wn * TR + rk] = rowminB;
   __syncthreads();
   {
     const int cc = col0 + t;
     if (cc < rows) {
-      const float a = fminf(s_cminA[t], s_cminA[TC + t]);
-      const float b = fminf(s_cminB[t], s_cminB[TC + t]);
-      if (a < inf) atomicMin(minbits + (long long)cc * n + rA, __float_as_uint(a));
-      if (b < inf) atomicMin(minbits + (long long)cc * n + rA + 1, __float_as_uint(b));
+      // a segment with no pair of different images is exactly +inf (masked): skip it,
+      // also because segment B may be the padding image n
+      const float a = nmin(s_cminA[t], s_cminA[TC + t]);
+      const float b = nmin(s_cminB[t], s_cminB[TC + t]);
+      if (a != inf) atomicMin(minbits + (long long)cc * n + rA, min_key(a));
+      if (b != inf) atomicMin(minbits + (long long)cc * n + rA + 1, min_key(b));
     }
   }
   if (t < TR) {
     const int r = row0 + t;
     if (r < rows) {
-      const float a = fminf(s_rminA[t], s_rminA[TR + t]);
-      const float b = fminf(s_rminB[t], s_rminB[TR + t]);
-      if (a < inf) atomicMin(minbits + (long long)r * n + cA, __float_as_uint(a));
-      if (b < inf) atomicMin(minbits + (long long)r * n + cA + 1, __float_as_uint(b));
+      const float a = nmin(s_rminA[t], s_rminA[TR + t]);
+      const float b = nmin(s_rminB[t], s_rminB[TR + t]);
+      if (a != inf) atomicMin(minbits + (long long)r * n + cA, min_key(a));
+      if (b != inf) atomicMin(minbits + (long long)r * n + cA + 1, min_key(b));
     }
   }
 }
@@ -475,7 +481,7 @@ inline void run_prepare(const float* z, int n, int p, int c, int normalize, void
   const Workspace w = carve(ws, n, p);
   hipLaunchKernelGGL(split_prepare_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, z, (int)rows, c,
                      nkb_of(c), normalize, w.norms, w.inv, split_array(ws, n, p));
-  launch_fill_u32(w.minbits, (size_t)rows * n, kInfBits, s);
+  launch_fill_u32(w.minbits, (size_t)rows * n, kMinFill, s);
 }
 
 inline int run_pairs(int n, int p, int c, void* ws, hipStream_t s) {

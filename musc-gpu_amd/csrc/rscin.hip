@@ -6,7 +6,9 @@
 // :8-11); the refined score of image i is sum_j W_ij s_j / sum_j W_ij over the
 // kept entries (the row-normalised D^-1 W times s, :12-18), averaged over k_list
 // (:20).  One workgroup per image i: similarities of row i into LDS, each kept
-// set found by rank counting (ties broken by column index), sums in fp64.
+// set found by rank counting (ties broken by column index), sums in fp64.  The
+// min-max normalisation propagates NaN like numpy's min/max (:27): one NaN raw
+// score makes every refined score NaN, as in the reference.
 #include "common.hpp"
 
 namespace musc {
@@ -15,6 +17,9 @@ namespace rscin {
 constexpr int kThreads = 256;
 constexpr int kMaxN = 4096;
 constexpr int kMaxK = 16;
+
+__device__ inline double nmin(double a, double b) { return __builtin_elementwise_minimum(a, b); }
+__device__ inline double nmax(double a, double b) { return __builtin_elementwise_maximum(a, b); }
 
 struct KList {
   int k[kMaxK];
@@ -31,13 +36,13 @@ __global__ __launch_bounds__(kThreads) void rscin_kernel(const float* __restrict
   // min / max of the raw scores
   double mn = INFINITY, mx = -INFINITY;
   for (int j = tid; j < n; j += kThreads) {
-    mn = fmin(mn, raw[j]);
-    mx = fmax(mx, raw[j]);
+    mn = nmin(mn, raw[j]);
+    mx = nmax(mx, raw[j]);
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
-    mn = fmin(mn, __shfl_xor(mn, off, kWave));
-    mx = fmax(mx, __shfl_xor(mx, off, kWave));
+    mn = nmin(mn, __shfl_xor(mn, off, kWave));
+    mx = nmax(mx, __shfl_xor(mx, off, kWave));
   }
   if (lane == 0) {
     red[0][wave] = mn;
@@ -47,8 +52,8 @@ __global__ __launch_bounds__(kThreads) void rscin_kernel(const float* __restrict
   if (tid == 0) {
     double a = red[0][0], b = red[1][0];
     for (int q = 1; q < kThreads / kWave; ++q) {
-      a = fmin(a, red[0][q]);
-      b = fmax(b, red[1][q]);
+      a = nmin(a, red[0][q]);
+      b = nmax(b, red[1][q]);
     }
     s_min = a;
     s_max = b;

@@ -7,8 +7,9 @@ accelerated path is unavailable; `configure_backend(cfg, device_type)` returns
 cfg itself or a deep-copied super_fast preset.
 
 The accelerated path here is libmusc_hip on a ROCm GPU, so the reference's
-Windows/NVRTC gate (:12-13) becomes "torch is a ROCm build and libmusc_hip.so
-loads".  `platform` is accepted for signature compatibility and ignored.
+Windows/NVRTC gate (:12-13) becomes "torch is a ROCm build, libmusc_hip.so loads
+and the current device has the architecture its kernels are compiled for".
+`platform` is accepted for signature compatibility and ignored.
 """
 from __future__ import annotations
 
@@ -28,7 +29,7 @@ def select_backend(requested, device_type, platform=None):
     if torch.version.hip is None:
         return 'original', 'the accelerated runtime requires a ROCm build of PyTorch'
     from . import _runtime
-    ok, reason = _runtime.available()
+    ok, reason = _runtime.device_supported()
     if not ok:
         return 'original', reason
     return requested, None

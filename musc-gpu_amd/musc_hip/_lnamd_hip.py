@@ -104,16 +104,29 @@ def lnamd(tokens: list[torch.Tensor], radii: list[int], *, l2norm: bool = False,
     return out
 
 
+# Limits of musc_lnamd_f32 itself (include/musc_hip.h): fp32/fp16 tokens on a ROCm
+# device, 4 <= C <= 4096 with C % 4 == 0, at most 16 layers, a grid side of 1..1024.
+MAX_LAYERS = 16
+MAX_CHANNELS = 4096
+MAX_SIDE = 1024
+
+
 def supported(layer, features: list[torch.Tensor]) -> bool:
-    """The reference's fast-path predicate (_encoder_gpu.py:18-21, _aggregation_cache.py:19-23)."""
+    """The reference's fast-path predicate (_encoder_gpu.py:18-21, _aggregation_cache.py:19-23),
+    narrowed by the kernel's own limits, so that every input the kernel would reject
+    takes layer._embed as in the reference instead of raising."""
     first = features[0]
     batch, length, channels = first.shape
     side = math.isqrt(length - 1)
-    return not (side * side != length - 1 or layer.patch_maker.stride != 1
-                or layer.r not in (1, 3, 5) or layer.LNA.output_dim != channels
-                or len(features) != len(layer.LNA.preprocessing_modules)
-                or any(t.shape != first.shape or t.dtype != first.dtype or t.device != first.device
-                       for t in features))
+    if (side * side != length - 1 or layer.patch_maker.stride != 1
+            or layer.r not in (1, 3, 5) or layer.LNA.output_dim != channels
+            or len(features) != len(layer.LNA.preprocessing_modules)
+            or any(t.shape != first.shape or t.dtype != first.dtype or t.device != first.device
+                   for t in features)):
+        return False
+    return (first.dtype in (torch.float32, torch.float16) and first.is_cuda and torch.version.hip is not None
+            and batch >= 1 and 4 <= channels <= MAX_CHANNELS and channels % 4 == 0
+            and 1 <= len(features) <= MAX_LAYERS and 1 <= side <= MAX_SIDE)
 
 
 class LNAMD:

@@ -44,6 +44,7 @@ _vp, _i, _f, _sz, _ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_
 SIGNATURES = {
     'musc_strerror': (ctypes.c_char_p, [_i]),
     'musc_version': (_i, []),
+    'musc_target_arch': (ctypes.c_char_p, []),
     'musc_msm_workspace_bytes': (_i, [_i, _i, _i, ctypes.POINTER(_sz)]),
     'musc_msm_scores_f32': (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
     'musc_msm_nearest_f32': (_i, [_vp, _i, _i, _i, _vp, _vp, _sz, _vp]),
@@ -114,6 +115,33 @@ def available() -> tuple[bool, str | None]:
         return True, None
     except LibraryUnavailable as exc:
         return False, str(exc)
+
+
+def target_arch() -> str:
+    """The architecture libmusc_hip.so's kernels are compiled for (e.g. 'gfx950')."""
+    return library().musc_target_arch().decode()
+
+
+def device_supported(device=None) -> tuple[bool, str | None]:
+    """(True, None) if the kernels can run on `device` (default: the current one).
+
+    Compares the device's architecture name (gcnArchName up to the first ':') with
+    the library's target; a mismatch would otherwise surface as an invalid-device-
+    function error at the first launch.
+    """
+    ok, reason = available()
+    if not ok:
+        return False, reason
+    if not torch.cuda.is_available():
+        return False, 'no ROCm device is visible'
+    index = torch.cuda.current_device() if device is None else torch.device(device).index
+    if index is None:
+        index = torch.cuda.current_device()
+    arch = str(getattr(torch.cuda.get_device_properties(index), 'gcnArchName', '')).split(':')[0]
+    want = target_arch()
+    if arch != want:
+        return False, f'libmusc_hip.so is built for {want}; device {index} is {arch or "of unknown architecture"}'
+    return True, None
 
 
 def strerror(rc: int) -> str:

@@ -25,8 +25,8 @@ HIPCC = os.environ.get('HIPCC', '/opt/rocm/bin/hipcc')
 # Packed FP32 instructions are disabled for all device code (they are emitted by
 # the compiler from ordinary float code otherwise).
 DEVICE_FLAGS = ['-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops']
-COMMON = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}', '-Wall', '-Wno-unused-function',
-          '-Wno-unused-variable', '-Wno-unused-but-set-variable'] + DEVICE_FLAGS
+COMMON = ['-O3', '-std=c++17', '-fPIC', f'--offload-arch={ARCH}', f'-DMUSC_TARGET_ARCH="{ARCH}"', '-Wall',
+          '-Wno-unused-function', '-Wno-unused-variable', '-Wno-unused-but-set-variable'] + DEVICE_FLAGS
 
 
 # Per-file device flags.  attention.hip: the online softmax rescales the MFMA

@@ -30,6 +30,7 @@ def c_oracle():
         lib.msm_nearest_f64.argtypes = [fp, ip, ip, ip, dp]
         lib.msm_scores_f64.argtypes = [fp, ip, ip, ip, ip, ip, dp]
         lib.msm_scores_from_nearest_f64.argtypes = [dp, ip, ip, ip, ip, dp]
+        lib.msm_nearest_rows_f64.argtypes = [fp, ip, ip, ip, dp, ip, dp]
         _LIB = lib
     return _LIB
 
@@ -54,4 +55,22 @@ def msm_nearest_f64_c(z):
     rc = c_oracle().msm_nearest_f64(z.ctypes.data, n, p, c, out.ctypes.data)
     if rc:
         raise RuntimeError(f'msm_nearest_f64 failed with code {rc}')
+    return out
+
+
+def msm_row_scores_f64_c(z, rows, a, b):
+    """float64 scores of selected global rows (i*p + q) of a float32 numpy array z (N, P, C),
+    from the C brute force over those rows only: (len(rows),) float64."""
+    import numpy as np
+    z = np.ascontiguousarray(z, dtype=np.float32)
+    n, p, c = z.shape
+    idx = np.ascontiguousarray(rows, dtype=np.int64)
+    near = np.empty((len(idx), n), dtype=np.float64)
+    rc = c_oracle().msm_nearest_rows_f64(z.ctypes.data, n, p, c, idx.ctypes.data, len(idx), near.ctypes.data)
+    if rc:
+        raise RuntimeError(f'msm_nearest_rows_f64 failed with code {rc}')
+    out = np.empty(len(idx))
+    for k, row in enumerate(idx):
+        vals = np.sort(np.delete(near[k], int(row) // p))        # NaN sorts last, as in torch.topk
+        out[k] = vals[a:b].mean()
     return out

@@ -62,11 +62,14 @@ def lnamd_embed(features: list[torch.Tensor], r: int) -> torch.Tensor:
     return stacked.reshape(b, -1, *stacked.shape[-2:]).detach()   # _LNAMD.py:127
 
 
-def aggregate_direct(features: list[torch.Tensor], r: int, eps: float = 1e-5) -> torch.Tensor:
-    """layer_norm + avg_pool2d(count_include_pad) identity: (B, T, C) list -> (B, P, L, C)."""
+def aggregate_direct(features: list[torch.Tensor], r: int, eps: float = 1e-5, device='cpu') -> torch.Tensor:
+    """layer_norm + avg_pool2d(count_include_pad) identity: (B, T, C) list -> (B, P, L, C).
+
+    Runs in fp32 on `device` (None: where the tokens live; full-size parity checks run
+    it on the GPU box's device, as the reference's accelerated aggregation does)."""
     values = []
     for f in features:
-        x = _spatial(f.detach().to('cpu', torch.float32))
+        x = _spatial(f.detach().to(f.device if device is None else device, torch.float32))
         x = F.layer_norm(x, x.shape[1:], None, None, eps)
         if r != 1:
             x = F.avg_pool2d(x, r, stride=1, padding=r // 2, count_include_pad=True)

@@ -71,6 +71,19 @@ def MSM(Z: torch.Tensor, topmin_min: float = 0, topmin_max: float = 0.3) -> torc
     return torch.stack(rows, 0)
 
 
+def MSM_device(Z: torch.Tensor, topmin_min: float = 0, topmin_max: float = 0.3) -> torch.Tensor:
+    """(N, P) float64 scores, the same restatement evaluated where Z lives.
+
+    For full-size parity checks on the GPU box: compute_scores_fast's torch calls
+    (cdist, min, topk, mean) run on Z's device in fp32, one query image at a time.
+    Tests pin this device run against the float64 brute force on sampled rows
+    (msm_row_scores_f64_c); matmul TF32/reduced-precision modes must be off.
+    """
+    Z = Z.detach().float().contiguous()
+    return torch.stack([compute_scores_fast(Z, i, topmin_min, topmin_max).double()
+                        for i in range(Z.shape[0])], 0)
+
+
 def nearest(Z: torch.Tensor) -> torch.Tensor:
     """(N*P, N) fp32 per-reference-image minima with +inf on the own image."""
     Z = Z.detach().to('cpu', torch.float32).contiguous()

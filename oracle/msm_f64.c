@@ -11,42 +11,64 @@
  * result is the mathematical value to ~1e-15 and pins both the torch-fp32
  * restatement (oracle/msm.py) and the HIP kernels.
  *
+ * NaN follows the reference's torch semantics: a NaN distance makes the minimum
+ * over that reference image NaN (torch.min propagates it, _MSM.py:17), and NaN
+ * minima sort after every number (torch.topk(largest=False), _MSM.py:27), so a
+ * NaN inside the rank window makes the mean NaN.
+ *
  * Build: see oracle/build.py (gcc -O3 -fopenmp -shared -fPIC).
  */
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
 
+/* One row's minima: out[j] = min_r ||z[row]-z[j,r]||, +inf for the row's own image. */
+static void nearest_row(const float* z, int n, int p, int c, long row, double* out) {
+  const int i = (int)(row / p);
+  const float* a = z + row * c;
+  for (int j = 0; j < n; ++j) {
+    double best = INFINITY;
+    if (j != i) {
+      for (int r = 0; r < p && !isnan(best); ++r) {
+        const float* b = z + ((long)j * p + r) * c;
+        double s = 0.0;
+        for (int k = 0; k < c; ++k) {
+          const double d = (double)a[k] - (double)b[k];
+          s += d * d;
+        }
+        if (isnan(s) || s < best) best = s;
+      }
+      best = sqrt(best);
+    }
+    out[j] = best;
+  }
+}
+
 /* nearest[(i*p+q)*n + j] = min_r ||z[i,q]-z[j,r]||, +inf for j == i. */
 int msm_nearest_f64(const float* z, int n, int p, int c, double* nearest) {
   if (!z || !nearest || n < 1 || p < 1 || c < 1) return 1;
   const long rows = (long)n * p;
 #pragma omp parallel for schedule(dynamic, 4)
-  for (long row = 0; row < rows; ++row) {
-    const int i = (int)(row / p);
-    const float* a = z + row * c;
-    for (int j = 0; j < n; ++j) {
-      double best = INFINITY;
-      if (j != i) {
-        for (int r = 0; r < p; ++r) {
-          const float* b = z + ((long)j * p + r) * c;
-          double s = 0.0;
-          for (int k = 0; k < c; ++k) {
-            const double d = (double)a[k] - (double)b[k];
-            s += d * d;
-          }
-          if (s < best) best = s;
-        }
-        best = sqrt(best);
-      }
-      nearest[row * n + j] = best;
-    }
-  }
+  for (long row = 0; row < rows; ++row) nearest_row(z, n, p, c, row, nearest + row * n);
   return 0;
 }
 
+/* The same for selected global rows only: out[k*n + j] is the minimum of row rows[k]
+ * (a row index i*p + q) against image j. */
+int msm_nearest_rows_f64(const float* z, int n, int p, int c, const long long* rows, int nrows, double* out) {
+  if (!z || !rows || !out || n < 1 || p < 1 || c < 1 || nrows < 0) return 1;
+  for (int k = 0; k < nrows; ++k)
+    if (rows[k] < 0 || rows[k] >= (long long)n * p) return 1;
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int k = 0; k < nrows; ++k) nearest_row(z, n, p, c, (long)rows[k], out + (long)k * n);
+  return 0;
+}
+
+/* Ascending, NaN after every number. */
 static int cmp_double(const void* x, const void* y) {
   const double a = *(const double*)x, b = *(const double*)y;
+  if (isnan(a)) return isnan(b) ? 0 : 1;
+  if (isnan(b)) return -1;
   return (a > b) - (a < b);
 }
 

@@ -169,3 +169,26 @@ def test_normalize_rows_equals_normalised_input(device):
     # without the flag the scores are those of the raw rows
     raw = _MSM_hip.MSM(z.to(device)).cpu().numpy()
     np.testing.assert_allclose(raw, om.MSM(z).numpy(), rtol=0, atol=1e-4)
+
+
+@pytest.mark.parametrize('n', [2, 3, 31, 32, 33, 64, 65, 96, 97, 128, 129, 160, 161, 192, 193, 200])
+def test_rank_selection_across_register_sizes(device, n):
+    # the rank kernel keeps a row's n minima in registers for n <= 192 (instantiations of
+    # 32/64/96/128/160/192 keys) and counts ranks in LDS beyond; every boundary, windows
+    # starting above 0, and ties.  Small-integer features make every norm and dot product
+    # exact in fp32, so both sides see the same squared distances (integers) and ties are
+    # exact: many equal minima, and image 1 duplicates image 0 (zero distances).
+    g = torch.Generator().manual_seed(n)
+    z = torch.randint(-2, 3, (n, 5, 12), generator=g).float()
+    if n >= 3:
+        z[1] = z[0]
+    zd = z.to(device)
+    windows = [(0, 0.3), (0, 1.0 - 1e-9), (0.1, 0.3)] if n >= 11 else [(0, n - 1)]
+    for lo, hi in windows:
+        a, b = om.rank_window(n, lo, hi)
+        if not 0 <= a < b <= n - 1:
+            continue
+        got = _MSM_hip.MSM(zd, topmin_min=lo, topmin_max=hi).cpu().numpy()
+        ref = om.MSM(z, lo, hi).numpy()
+        err = np.abs(got - ref).max()
+        assert err <= ATOL, (n, lo, hi, err)

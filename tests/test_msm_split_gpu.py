@@ -78,8 +78,9 @@ def _split_minima(z: torch.Tensor, normalize: bool) -> np.ndarray:
     torch.cuda.synchronize()
     rows = n * p
     off = 2 * ((rows * 4 + 255) // 256 * 256)
-    bits = ws[off:off + rows * n * 4].view(torch.int32).cpu().numpy().view(np.uint32)
-    return bits.view(np.float32).reshape(rows, n)
+    keys = ws[off:off + rows * n * 4].view(torch.int32).cpu().numpy().view(np.uint32)
+    # the buffer holds min keys: key - 1 is the squared minimum's bits (0xffffffff: NaN)
+    return (keys - np.uint32(1)).view(np.float32).reshape(rows, n)
 
 
 def test_minima_vs_f64_bruteforce(device):
