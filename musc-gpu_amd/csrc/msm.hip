@@ -503,18 +503,41 @@ constexpr uint32_t kNoKey = 0xffffffffu;  // NaN minimum, own image, or padding
 
 // One thread per row, its n keys in registers (n <= kKeys).  t is found by a binary
 // search over the key bits: the largest t with #{key < t} < k, built from the most
-// significant bit down (32 steps of one compare and one add per key).  Rows sit
-// n * 4 bytes apart, so the loads of a wave cover one contiguous range.
+// significant bit down (32 steps of one compare and one add per key).  A workgroup is
+// one wave of 64 consecutive rows, whose keys are one contiguous range: it is staged
+// in LDS with coalesced 16-byte loads, then lane t reads its row starting at key t % n
+// (the order of a row's keys in registers does not matter), so that lanes whose rows
+// start in the same bank (n a multiple of the bank count) still read distinct banks.
+constexpr int kRankRows = 64;
+
 template <int kKeys>
-__global__ __launch_bounds__(64) void msm_rank_select_kernel(const uint32_t* __restrict__ minbits, int rows, int n,
-                                                             int p, int a, int b, double* __restrict__ scores) {
-  const long long row = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (row >= rows) return;
+__global__ __launch_bounds__(kRankRows) void msm_rank_select_kernel(const uint32_t* __restrict__ minbits, int rows,
+                                                                    int n, int p, int a, int b,
+                                                                    double* __restrict__ scores) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t s_rowkeys[];  // kRankRows * n
+  const int t = threadIdx.x;
+  const long long row0 = (long long)blockIdx.x * kRankRows;
+  const int nrows = (int)min((long long)kRankRows, rows - row0);
+  const int count = nrows * n;  // keys of this workgroup's rows
+  const uint32_t* src = minbits + row0 * n;
+  // row0 * n * 4 bytes is a multiple of 256: 16-byte loads are aligned
+  const int n4 = count / 4;
+  for (int i = t; i < n4; i += kRankRows)
+    reinterpret_cast<uint4*>(s_rowkeys)[i] = reinterpret_cast<const uint4*>(src)[i];
+  for (int i = 4 * n4 + t; i < count; i += kRankRows) s_rowkeys[i] = src[i];
+  __syncthreads();
+  if (t >= nrows) return;
+  const long long row = row0 + t;
   const int self = (int)(row / p);
-  const uint32_t* src = minbits + row * n;
+  const uint32_t* mine = s_rowkeys + t * n;
   uint32_t key[kKeys];
+  int j = t % n;  // image of the key in slot s: (t + s) % n
 #pragma unroll
-  for (int j = 0; j < kKeys; ++j) key[j] = (j < n && j != self) ? key_bits(src[j]) : kNoKey;
+  for (int s = 0; s < kKeys; ++s) {
+    const uint32_t v = mine[j];  // j < n always: every read is in range, none is branched around
+    key[s] = (s < n && j != self) ? key_bits(v) : kNoKey;
+    j = j + 1 == n ? 0 : j + 1;
+  }
   uint32_t ta = 0, tb = 0;  // a-th and b-th smallest keys (ta stays 0 for a = 0)
   if (a == 0) {
 #pragma unroll 1
@@ -522,7 +545,7 @@ __global__ __launch_bounds__(64) void msm_rank_select_kernel(const uint32_t* __r
       const uint32_t cb = tb | (1u << bit);
       int nb = 0;
 #pragma unroll
-      for (int j = 0; j < kKeys; ++j) nb += key[j] < cb;
+      for (int q = 0; q < kKeys; ++q) nb += key[q] < cb;
       tb = nb < b ? cb : tb;
     }
   } else {
@@ -531,9 +554,9 @@ __global__ __launch_bounds__(64) void msm_rank_select_kernel(const uint32_t* __r
       const uint32_t ca = ta | (1u << bit), cb = tb | (1u << bit);
       int na = 0, nb = 0;
 #pragma unroll
-      for (int j = 0; j < kKeys; ++j) {
-        na += key[j] < ca;
-        nb += key[j] < cb;
+      for (int q = 0; q < kKeys; ++q) {
+        na += key[q] < ca;
+        nb += key[q] < cb;
       }
       ta = na < a ? ca : ta;
       tb = nb < b ? cb : tb;
@@ -542,13 +565,13 @@ __global__ __launch_bounds__(64) void msm_rank_select_kernel(const uint32_t* __r
   double sa = 0.0, sb = 0.0;
   int la = 0, lb = 0;
 #pragma unroll
-  for (int j = 0; j < kKeys; ++j) {
-    const double r = (double)sqrtf(__uint_as_float(key[j]));
-    if (key[j] < tb) {
+  for (int q = 0; q < kKeys; ++q) {
+    const double r = (double)sqrtf(__uint_as_float(key[q]));
+    if (key[q] < tb) {
       sb += r;
       ++lb;
     }
-    if (key[j] < ta) {
+    if (key[q] < ta) {
       sa += r;
       ++la;
     }
@@ -648,9 +671,10 @@ inline int run_pairs(const float* z, int n, int p, int c, const Workspace& w, hi
 int run_rank(int n, int p, int a, int b, double* scores, const Workspace& w, hipStream_t s) {
   const long long rows = (long long)n * p;
   if (n <= kMaxSelectKeys) {
-    const dim3 grid((unsigned)((rows + 63) / 64)), block(64);
+    const dim3 grid((unsigned)((rows + kRankRows - 1) / kRankRows)), block(kRankRows);
+    const size_t smem = (size_t)kRankRows * n * sizeof(uint32_t);  // <= 48 KB
 #define MUSC_RANK_LAUNCH(K) \
-  hipLaunchKernelGGL(msm_rank_select_kernel<K>, grid, block, 0, s, w.minbits, (int)rows, n, p, a, b, scores)
+  hipLaunchKernelGGL(msm_rank_select_kernel<K>, grid, block, smem, s, w.minbits, (int)rows, n, p, a, b, scores)
     if (n <= 32) MUSC_RANK_LAUNCH(32);
     else if (n <= 64) MUSC_RANK_LAUNCH(64);
     else if (n <= 96) MUSC_RANK_LAUNCH(96);
