@@ -39,6 +39,7 @@ extern "C" {
 #define MUSC_ERR_INVALID_ARG    1001  /* bad shape, rank window, null pointer */
 #define MUSC_ERR_WORKSPACE      1002  /* workspace smaller than required      */
 #define MUSC_ERR_UNSUPPORTED    1003  /* shape outside the implemented range  */
+#define MUSC_ERR_SCRATCH_LIMIT  1004  /* needs more than the no-allocation scratch */
 
 /* Text for any return code of this library (never NULL). */
 const char* musc_strerror(int code);
@@ -80,6 +81,21 @@ int musc_msm_scores_f32(const float* z, int n, int p, int c,
                         int rank_lo, int rank_hi, double* scores,
                         void* workspace, size_t workspace_bytes,
                         hipStream_t stream);
+
+/* musc_msm_scores_f32 without a workspace argument and without allocating: no
+ * counterpart in the reference.  For callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The workspace is a device array inside the library, one per GPU,
+ * of MUSC_NOALLOC_SCRATCH_BYTES (64 MiB; held by every GPU the library runs on
+ * until the process ends), so pools whose musc_msm_workspace_bytes exceeds it are
+ * rejected with MUSC_ERR_SCRATCH_LIMIT (N = 83, P = 1369 needs 38.6 MB; N = 160,
+ * P = 1369 does not fit).  Runs on the current device; `stream` must belong to it.
+ * Every call on one GPU uses that GPU's array: calls that overlap on one GPU (other
+ * streams or threads) race and must be serialised by the caller.  Same arguments
+ * (minus the workspace), results and errors as musc_msm_scores_f32. */
+#define MUSC_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int musc_msm_scores_f32_noalloc(const float* z, int n, int p, int c, int rank_lo, int rank_hi,
+                                double* scores, hipStream_t stream);
 
 /* Per-reference-image nearest distances, the intermediate of the scoring:
  *   nearest (n*p, n) fp32 out, nearest[i*p+q][j] = min_r ||z[i,q]-z[j,r]||_2

@@ -7,6 +7,9 @@ extern "C" const char* musc_strerror(int code) {
     case MUSC_ERR_INVALID_ARG: return "musc: invalid argument (shape, rank window, pointer or alignment)";
     case MUSC_ERR_WORKSPACE: return "musc: workspace is missing or smaller than required";
     case MUSC_ERR_UNSUPPORTED: return "musc: shape outside the implemented range";
+    case MUSC_ERR_SCRATCH_LIMIT:
+      return "musc: the problem's workspace exceeds the no-allocation scratch (MUSC_NOALLOC_SCRATCH_BYTES = 64 MiB); "
+             "use the entry point that takes a workspace";
     default: break;
   }
   if (code > 0 && code < 1000) return hipGetErrorString(static_cast<hipError_t>(code));

@@ -24,6 +24,8 @@
 //                            of the n-1 minima (NaN last) by a binary search over
 //                            the key bits, then the mean of the square roots of
 //                            ranks [a, b).
+#include <mutex>
+
 #include "msm_common.hpp"
 
 namespace musc {
@@ -736,6 +738,54 @@ extern "C" int musc_msm_scores_f32(const float* z, int n, int p, int c, int rank
   rc = msm::run_pairs(z, n, p, c, w, stream);
   if (rc) return rc;
   return msm::run_rank(n, p, rank_lo, rank_hi, scores, w, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Scores without allocation: the workspace of musc_msm_scores_f32 lives in a
+// file-scope device array (one per GPU, for the life of the process), for callers
+// that cannot allocate.  Host code never passes the array's name to a kernel: its
+// device address comes from hipGetSymbolAddress, once per device.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr size_t kScratchBytes = size_t(64) << 20;  // MUSC_NOALLOC_SCRATCH_BYTES
+static_assert(kScratchBytes == MUSC_NOALLOC_SCRATCH_BYTES, "header and library disagree on the scratch size");
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices];  // device address of `scratch` per device, set on first use
+
+// Device address of the current device's scratch array.
+int current_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxScratchDevices) return MUSC_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (!ptr) return MUSC_ERR_UNSUPPORTED;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MUSC_OK;
+}
+
+}  // namespace
+
+extern "C" int musc_msm_scores_f32_noalloc(const float* z, int n, int p, int c, int rank_lo, int rank_hi,
+                                           double* scores, hipStream_t stream) {
+  if (!z || n < 2 || p < 1 || c < 1) return MUSC_ERR_INVALID_ARG;
+  if ((long long)n * p > (1LL << 30) || n > 4096) return MUSC_ERR_UNSUPPORTED;
+  if (msm::workspace_bytes(n, p) > kScratchBytes) return MUSC_ERR_SCRATCH_LIMIT;
+  void* ws = nullptr;
+  const int rc = current_scratch(&ws);
+  if (rc) return rc;
+  // the minima keys are refilled by every call (prepare); nothing else carries over
+  return musc_msm_scores_f32(z, n, p, c, rank_lo, rank_hi, scores, ws, kScratchBytes, stream);
 }
 
 extern "C" int musc_msm_nearest_f32(const float* z, int n, int p, int c, float* nearest, void* workspace,

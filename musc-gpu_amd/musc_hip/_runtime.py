@@ -27,6 +27,7 @@ MUSC_OK = 0
 MUSC_ERR_INVALID_ARG = 1001
 MUSC_ERR_WORKSPACE = 1002
 MUSC_ERR_UNSUPPORTED = 1003
+MUSC_ERR_SCRATCH_LIMIT = 1004
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -47,6 +48,7 @@ SIGNATURES = {
     'musc_target_arch': (ctypes.c_char_p, []),
     'musc_msm_workspace_bytes': (_i, [_i, _i, _i, ctypes.POINTER(_sz)]),
     'musc_msm_scores_f32': (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _sz, _vp]),
+    'musc_msm_scores_f32_noalloc': (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp]),
     'musc_msm_nearest_f32': (_i, [_vp, _i, _i, _i, _vp, _vp, _sz, _vp]),
     'musc_msm_prepare_f32': (_i, [_vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     'musc_msm_pair_minima_f32': (_i, [_vp, _i, _i, _i, _vp, _sz, _vp]),
