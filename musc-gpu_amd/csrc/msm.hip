@@ -20,10 +20,11 @@
 //                            with unsigned atomicMin on an order-preserving key
 //                            in which NaN wins (min_key, msm_common.hpp).
 //                            The distance matrix never reaches HBM.
-//   4. msm_rank_select_kernel  one thread per patch: the a-th and b-th smallest
-//                            of the n-1 minima (NaN last) by a binary search over
-//                            the key bits, then the mean of the square roots of
-//                            ranks [a, b).
+//   4. msm_rank_*_kernel     one thread per patch ranks the n-1 minima (NaN last)
+//                            and averages the square roots of ranks [a, b): a
+//                            sorted register list of the b smallest (b <= 32), or
+//                            the a-th and b-th smallest by a binary search over
+//                            the key bits.
 #include <mutex>
 
 #include "msm_common.hpp"
@@ -583,6 +584,53 @@ __global__ __launch_bounds__(kRankRows) void msm_rank_select_kernel(const uint32
   scores[row] = (double)(float)((sb - sa) / (double)(b - a));
 }
 
+// Short windows (b <= 32, every BASELINE configuration): one thread per row keeps the
+// kList smallest keys seen so far in an ascending register list; each of the row's n
+// keys is inserted by a min/max pass down the list (2 kList instructions per key,
+// against 64 per register slot for the bit search), and ranks [a, b) are read off the
+// list.  Staging as in msm_rank_select_kernel.
+template <int kList>
+__global__ __launch_bounds__(kRankRows) void msm_rank_insert_kernel(const uint32_t* __restrict__ minbits, int rows,
+                                                                    int n, int p, int a, int b,
+                                                                    double* __restrict__ scores) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t s_rowkeys[];  // kRankRows * n
+  const int t = threadIdx.x;
+  const long long row0 = (long long)blockIdx.x * kRankRows;
+  const int nrows = (int)min((long long)kRankRows, rows - row0);
+  const int count = nrows * n;
+  const uint32_t* src = minbits + row0 * n;
+  const int n4 = count / 4;
+  for (int i = t; i < n4; i += kRankRows)
+    reinterpret_cast<uint4*>(s_rowkeys)[i] = reinterpret_cast<const uint4*>(src)[i];
+  for (int i = 4 * n4 + t; i < count; i += kRankRows) s_rowkeys[i] = src[i];
+  __syncthreads();
+  if (t >= nrows) return;
+  const long long row = row0 + t;
+  const int self = (int)(row / p);
+  const uint32_t* mine = s_rowkeys + t * n;
+  uint32_t list[kList];
+#pragma unroll
+  for (int i = 0; i < kList; ++i) list[i] = kNoKey;
+  int j = t % n;  // start at key t % n: see msm_rank_select_kernel
+#pragma unroll 2
+  for (int q = 0; q < n; ++q) {
+    const uint32_t v = mine[j];
+    uint32_t x = j != self ? key_bits(v) : kNoKey;  // the own image inserts nothing
+#pragma unroll
+    for (int i = 0; i < kList; ++i) {
+      const uint32_t lo = min(list[i], x);
+      x = max(list[i], x);
+      list[i] = lo;
+    }
+    j = j + 1 == n ? 0 : j + 1;
+  }
+  double sum = 0.0;
+#pragma unroll
+  for (int i = 0; i < kList; ++i)
+    if (i >= a && i < b) sum += (double)sqrtf(__uint_as_float(list[i]));
+  scores[row] = (double)(float)(sum / (double)(b - a));
+}
+
 // Rows of more than 192 images: one wave per row, the n keys staged in LDS and each
 // key's rank counted (ties broken by image index).
 constexpr int kRankWaves = 4;
@@ -672,6 +720,18 @@ inline int run_pairs(const float* z, int n, int p, int c, const Workspace& w, hi
 // Stage 3: trimmed rank means.
 int run_rank(int n, int p, int a, int b, double* scores, const Workspace& w, hipStream_t s) {
   const long long rows = (long long)n * p;
+  if (n <= kMaxSelectKeys && b <= 32) {
+    const dim3 grid((unsigned)((rows + kRankRows - 1) / kRankRows)), block(kRankRows);
+    const size_t smem = (size_t)kRankRows * n * sizeof(uint32_t);  // <= 48 KB
+#define MUSC_RANK_INSERT(K) \
+  hipLaunchKernelGGL(msm_rank_insert_kernel<K>, grid, block, smem, s, w.minbits, (int)rows, n, p, a, b, scores)
+    if (b <= 8) MUSC_RANK_INSERT(8);
+    else if (b <= 16) MUSC_RANK_INSERT(16);
+    else if (b <= 24) MUSC_RANK_INSERT(24);
+    else MUSC_RANK_INSERT(32);
+#undef MUSC_RANK_INSERT
+    return check_launch();
+  }
   if (n <= kMaxSelectKeys) {
     const dim3 grid((unsigned)((rows + kRankRows - 1) / kRankRows)), block(kRankRows);
     const size_t smem = (size_t)kRankRows * n * sizeof(uint32_t);  // <= 48 KB
