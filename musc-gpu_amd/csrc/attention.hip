@@ -332,11 +332,20 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
       *reinterpret_cast<half2v*>(&Vt[buf][(4 * dg + i) * VP16 + 2 * kp]) = pr;
     }
   };
-  // S^T of one staged key block (4 MFMAs over d = 64)
-  auto logits = [&](int buf) -> floatx16 {
+  // S^T of one staged key block (4 MFMAs over d = 64) plus one MFMA that adds -base to
+  // every logit: the A operand's k column 0 is 1 for every key, the B operand's k row 0
+  // holds -base for every query (this lane's running maximum as of the issue).  The
+  // logits come out shifted, so the softmax needs no subtraction per logit; base is an
+  // integer of at most 2048 in magnitude (exact in fp16) or 0.
+  half8 ones_col = {};
+  ones_col[0] = lh == 0 ? (_Float16)1.f : (_Float16)0.f;
+  auto logits = [&](int buf, float base) -> floatx16 {
+    half8 shift_row = {};
+    shift_row[0] = lh == 0 ? (_Float16)(-base) : (_Float16)0.f;
     floatx16 r;
 #pragma unroll
     for (int v = 0; v < 16; ++v) r[v] = 0.f;
+    r = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones_col, shift_row, r, 0, 0, 0);
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const half8 a = *reinterpret_cast<const half8*>(&Ks[buf][lq * KP16 + 16 * m + 8 * lh]);
@@ -344,19 +353,26 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
     }
     return r;
   };
+  // The running maximum is kept an integer while |m_run| <= 2048 (raised to the next
+  // integer, which only lowers the exponentials), so that it is exact as an fp16 base.
+  constexpr float kBaseLimit = 2048.f;
+  auto issue_base = [&]() { return fabsf(m_run) <= kBaseLimit ? m_run : 0.f; };  // -inf -> 0
 
-  // Software-pipelined key loop: iteration kb issues the logits MFMAs of block kb+1
-  // beside the softmax of block kb and its P V MFMAs, so each wave has independent
-  // matrix work while its exponentials and conversions run (this kernel has only
-  // ~2.75 waves per SIMD to hide that chain).  LDS holds K one block ahead of V.
+  // Software-pipelined key loop: step kb issues the logits MFMAs of block kb+1 beside
+  // the softmax of block kb and its P V MFMAs, so each wave has independent matrix
+  // work while its exponentials and conversions run (this kernel has only ~2.75 waves
+  // per SIMD to hide that chain).  LDS holds K one block ahead of V.  Steps alternate
+  // between two logits register sets (no copy per block).
   half8 kreg = load_k(0);
   store_k(0, kreg);
   half4 v0 = load_v(0, 0), v1 = load_v(0, 1);
   if (nkb > 1) kreg = load_k(1);
   __syncthreads();
-  floatx16 s = logits(0);
+  float base_a = issue_base(), base_b = 0.f;
+  floatx16 sa = logits(0, base_a), sb;
 
-  auto step = [&](int kb, auto more_c) {
+  // s holds the logits of block kb minus `base`; the next block's go into sn / bn.
+  auto step = [&](int kb, floatx16& s, float base, floatx16& sn, float& bn, auto more_c) {
     constexpr bool kMore = decltype(more_c)::value;
     if constexpr (kMore) store_k((kb + 1) & 1, kreg);
     store_v(kb & 1, v0, v1);
@@ -366,8 +382,10 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
       v1 = load_v(kb + 1, 1);
     }
     __syncthreads();
-    floatx16 sn;
-    if constexpr (kMore) sn = logits((kb + 1) & 1);
+    if constexpr (kMore) {
+      bn = issue_base();
+      sn = logits((kb + 1) & 1, bn);
+    }
     if constexpr (!kMore) {
       if ((kb + 1) * KB > t) {  // only the last block is ragged
 #pragma unroll
@@ -378,10 +396,11 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
     float bmax = s[0];
 #pragma unroll
     for (int v = 1; v < 16; ++v) bmax = fmaxf(bmax, s[v]);
-    bmax = halves_max(bmax);
+    bmax = halves_max(bmax) + base;  // this block's maximum logit
     // lazy rescaling (see kLazyLog2)
     if (!__all(bmax <= m_run + kLazyLog2)) {
-      const float mnew = fmaxf(m_run, bmax);
+      float mnew = fmaxf(m_run, bmax);
+      if (fabsf(mnew) <= kBaseLimit) mnew = ceilf(mnew);
       const float alpha = softmax_exp2(m_run - mnew);  // 0 on the first block (m_run = -inf)
       l_run *= alpha;
 #pragma unroll
@@ -391,16 +410,26 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
       }
       m_run = mnew;
     }
-    float psum = 0.f;
+    // re-base the logits when the running maximum moved since they were issued (the
+    // first blocks, the rare lazy raises, and every block once |m_run| > 2048)
+    const float shift = base - m_run;
+    if (__any(shift != 0.f)) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) s[v] += shift;
+    }
     half8 pf[2];
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const float e = softmax_exp2(s[v] - m_run);
-      psum += e;
-      pf[v >> 3][v & 7] = (_Float16)e;
+    for (int v = 0; v < 16; ++v) pf[v >> 3][v & 7] = (_Float16)softmax_exp2(s[v]);
+    // the row sum of the fp16 probabilities the P V product uses, two at a time in fp32
+    typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+    const half2v ones = {(_Float16)1.f, (_Float16)1.f};
+    float ps0 = 0.f, ps1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ps0 = __builtin_amdgcn_fdot2(half2v{pf[0][2 * i], pf[0][2 * i + 1]}, ones, ps0, false);
+      ps1 = __builtin_amdgcn_fdot2(half2v{pf[1][2 * i], pf[1][2 * i + 1]}, ones, ps1, false);
     }
-    psum = halves_sum(psum);
-    l_run += psum;
+    l_run += halves_sum(ps0 + ps1);
     const int vb = kb & 1;
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
@@ -413,10 +442,20 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
       o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, pf[mm], o0, 0, 0, 0);
       o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, pf[mm], o1, 0, 0, 0);
     }
-    if constexpr (kMore) s = sn;
   };
-  for (int kb = 0; kb + 1 < nkb; ++kb) step(kb, std::integral_constant<bool, true>{});
-  step(nkb - 1, std::integral_constant<bool, false>{});
+  using More = std::integral_constant<bool, true>;
+  using Last = std::integral_constant<bool, false>;
+  int kb = 0;
+  for (; kb + 2 < nkb; kb += 2) {
+    step(kb, sa, base_a, sb, base_b, More{});
+    step(kb + 1, sb, base_b, sa, base_a, More{});
+  }
+  if (kb + 1 < nkb) {
+    step(kb, sa, base_a, sb, base_b, More{});
+    step(kb + 1, sb, base_b, sa, base_a, Last{});
+  } else {
+    step(kb, sa, base_a, sb, base_b, Last{});
+  }
 
   if (q < t) {
     const float inv = 1.f / l_run;
