@@ -62,6 +62,17 @@ __device__ inline float halves_sum(float v) {
 // read in place with st = batch*3*heads*64, sb = 3*heads*64, sh = 64.
 constexpr int kBufferFlags = 0x00020000;  // buffer resource word 3 for raw byte-addressed loads
 
+// Forward work unit of workgroup blockIdx.x: (head, query tile), or x = -1 for the
+// grid's padding.  Units are numbered head-major, so the query tiles of one head are
+// consecutive logical ids, which xcd_logical_id places on one XCD: that XCD's L2 then
+// serves the head's K and V blocks to all of its query tiles.
+__device__ inline int2 fwd_unit(int t, int nbh) {
+  const int nqt = (t + QW * WAVES - 1) / (QW * WAVES);
+  const long long u = xcd_logical_id(blockIdx.x, gridDim.x);
+  if (u >= (long long)nqt * nbh) return make_int2(-1, 0);
+  return make_int2((int)(u / nqt), (int)(u % nqt));
+}
+
 struct HeadLayout {
   long long sb, sh, st;
   int heads;
@@ -103,14 +114,16 @@ __global__ __launch_bounds__(WAVES * kWave, 3) void attn_fwd_kernel(const float*
                                                                  const float* __restrict__ kg,
                                                                  const float* __restrict__ vg,
                                                                  float* __restrict__ og, int t, float scale_log2,
-                                                                 HeadLayout in, HeadLayout out) {
+                                                                 HeadLayout in, HeadLayout out, int nbh) {
   __shared__ __attribute__((aligned(16))) float Ks[2][KB * KPITCH];
   __shared__ __attribute__((aligned(16))) float Vt[2][D * VPITCH];
 
-  const int bh = blockIdx.y;
+  const int2 unit = fwd_unit(t, nbh);
+  if (unit.x < 0) return;
+  const int bh = unit.x;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int lq = lane & 31, lh = lane >> 5;
-  const int q = blockIdx.x * (QW * WAVES) + wave * QW + lq;
+  const int q = unit.y * (QW * WAVES) + wave * QW + lq;
   const long long head = in.base(bh), st = in.st;
 
   // This lane's query row, pre-scaled by scale*log2(e): qr[s][j] = q[8s + 4h + j].
@@ -269,14 +282,16 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
                                                                      const _Float16* __restrict__ vg,
                                                                      _Float16* __restrict__ og, int t,
                                                                      float scale_log2, HeadLayout in,
-                                                                     HeadLayout out) {
+                                                                     HeadLayout out, int nbh) {
   __shared__ __attribute__((aligned(16))) _Float16 Ks[2][KB * KP16];
   __shared__ __attribute__((aligned(16))) _Float16 Vt[2][D * VP16];
 
-  const int bh = blockIdx.y;
+  const int2 unit = fwd_unit(t, nbh);
+  if (unit.x < 0) return;
+  const int bh = unit.x;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int lq = lane & 31, lh = lane >> 5;
-  const int q = blockIdx.x * (QW * WAVES) + wave * QW + lq;
+  const int q = unit.y * (QW * WAVES) + wave * QW + lq;
   const long long head = in.base(bh), st = in.st;
 
   half8 qf[4];
@@ -664,15 +679,17 @@ int attention_fwd(const void* q, const void* k, const void* v, void* out, int dt
   if (!layout_ok(in, dtype) || !layout_ok(ol, dtype)) return MUSC_ERR_INVALID_ARG;
   if ((long long)batch * heads > 65535) return MUSC_ERR_UNSUPPORTED;
   const float scale_log2 = scale * 1.4426950408889634f;
-  dim3 grid((t + attn::QW * attn::WAVES - 1) / (attn::QW * attn::WAVES), batch * heads);
+  const int nbh = batch * heads;
+  const long long units = (long long)((t + attn::QW * attn::WAVES - 1) / (attn::QW * attn::WAVES)) * nbh;
+  const dim3 grid((unsigned)align_up((size_t)units, kXcds));
   if (dtype == MUSC_DTYPE_F32)
     hipLaunchKernelGGL(attn::attn_fwd_kernel, grid, dim3(attn::WAVES * kWave), 0, stream,
                        static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
-                       static_cast<float*>(out), t, scale_log2, in, ol);
+                       static_cast<float*>(out), t, scale_log2, in, ol, nbh);
   else
     hipLaunchKernelGGL(attn::attn_fwd_f16_kernel, grid, dim3(attn::WAVES * kWave), 0, stream,
                        static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
-                       static_cast<const _Float16*>(v), static_cast<_Float16*>(out), t, scale_log2, in, ol);
+                       static_cast<const _Float16*>(v), static_cast<_Float16*>(out), t, scale_log2, in, ol, nbh);
   return check_launch();
 }
 
