@@ -286,12 +286,8 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
         for (int v = 0; v < 16; ++v) m = nmin(m, d2[mb][nb][v]);
       cmin[nb] = m;
     }
-    {
-      // half lh keeps column block nb = lh and receives the other half's value for it
-      const float send = lh ? cmin[0] : cmin[1];
-      const float keep = lh ? cmin[1] : cmin[0];
-      cmin[0] = nmin(keep, __shfl_xor(send, 32, kWave));
-    }
+    // half lh keeps column block nb = lh, with the other half's minimum for it
+    cmin[0] = halves_min2(cmin[0], cmin[1]);
     // row minima over this wave's 64 columns: min over nb in-lane, then a transposing
     // butterfly over the 32 lanes of each half (31 exchanges); lane lr ends with the
     // minimum of value index k = lr, i.e. row (lr/16)*32 + ((lr%16)/4)*8 + lh*4 + lr%4.
@@ -317,14 +313,23 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
   }
 
   if constexpr (kSplit) {
-    // Two-segment register epilogue.  Rows of this tile belong to image rA (local
-    // index below the boundary) or rA + 1, columns to cA or cA + 1; padding rows
-    // and columns carry image n.  Same-image and padding pairs are masked to +inf,
-    // then row and column minima are taken per segment of the other dimension.
+    // Two-segment register epilogue (P >= 128, so a 128-row or 128-column range holds
+    // at most one image boundary).  Tile rows [0, rsplit) belong to image rA, rows
+    // [rsplit, BM) to image rA + 1 or to the padding (image n); columns likewise with
+    // csplit and cA.  Whether a pair is masked (same image, or padding) depends only
+    // on the segments of its row and column, so minima are taken per segment over the
+    // raw distances and a masked segment pair is replaced by +inf afterwards, the same
+    // as masking every distance first (min over +inf only).  A wave whose 64 rows (or
+    // columns) lie in one segment reduces them without per-distance selects.
     const float inf = __int_as_float(kInfBits);
     const int rA = rimg0, cA = cimg0;
+    const int rsplit = min(BM, min((rA + 1) * p, rows) - row0);
+    const int csplit = min(BN, min((cA + 1) * p, rows) - col0);
+    const int rBimg = row0 + rsplit < rows ? rA + 1 : n;  // used only when segment B is not empty
+    const int cBimg = col0 + csplit < rows ? cA + 1 : n;
+    const bool mAA = rA == cA, mAB = cBimg == n || rA == cBimg;
+    const bool mBA = rBimg == n || rBimg == cA, mBB = rBimg == n || cBimg == n || rBimg == cBimg;
     float d2[2][2][16];
-    bool rowB[2][16];  // row lies in segment B (image rA + 1)
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -332,88 +337,115 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
         const int i0 = wm * 64 + mb * 32 + g * 8 + lh * 4;
         const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[i0]);
         const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[i0]);
-        const int4 rim = *reinterpret_cast<const int4*>(&s_rimg[i0]);
         const float rv[4] = {rn.x, rn.y, rn.z, rn.w};
         const float rs[4] = {-2.f * ri.x, -2.f * ri.y, -2.f * ri.z, -2.f * ri.w};
-        const int rimg[4] = {rim.x, rim.y, rim.z, rim.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) rowB[mb][g * 4 + e] = rimg[e] != rA;
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-          const int j = wn * 64 + nb * 32 + lr;
-          const float cn = s_cnorm[j];
-          const float ci = s_cinv[j];
-          const int cimg = s_cimg[j];
+          const float cn = s_cnorm[wn * 64 + nb * 32 + lr];
+          const float ci = s_cinv[wn * 64 + nb * 32 + lr];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float v = fmaf(rs[e] * ci, acc[mb][nb][g * 4 + e], rv[e] + cn);  // clamped after the minima
-            const bool masked = rimg[e] == cimg || rimg[e] == n || cimg == n;
-            d2[mb][nb][g * 4 + e] = masked ? inf : v;
-          }
+          for (int e = 0; e < 4; ++e)  // clamped at 0 after the minima
+            d2[mb][nb][g * 4 + e] = fmaf(rs[e] * ci, acc[mb][nb][g * 4 + e], rv[e] + cn);
         }
       }
     // column minima over this wave's 64 rows, per row segment, then across lane halves
+    const int wr0 = wm * 64, wc0 = wn * 64;
     float cminA[2], cminB[2];
+    if (rsplit >= wr0 + 64 || rsplit <= wr0) {
+      float m[2];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      float a = inf, b = inf;
+      for (int nb = 0; nb < 2; ++nb) {
+        float x = d2[0][nb][0];
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+        for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float x = d2[mb][nb][v];
-          a = rowB[mb][v] ? a : nmin(a, x);
-          b = rowB[mb][v] ? nmin(b, x) : b;
-        }
-      cminA[nb] = a;
-      cminB[nb] = b;
+          for (int v = 0; v < 16; ++v) x = nmin(x, d2[mb][nb][v]);
+        m[nb] = x;
+      }
+      const bool inA = rsplit > wr0;
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        cminA[nb] = inA ? m[nb] : inf;
+        cminB[nb] = inA ? inf : m[nb];
+      }
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        float a = inf, b = inf;
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const bool inB = wr0 + mb * 32 + (v >> 2) * 8 + lh * 4 + (v & 3) >= rsplit;
+            a = nmin(a, inB ? inf : d2[mb][nb][v]);
+            b = nmin(b, inB ? d2[mb][nb][v] : inf);
+          }
+        cminA[nb] = a;
+        cminB[nb] = b;
+      }
     }
+    float colA = halves_min2(cminA[0], cminA[1]);  // column wc0 + lh * 32 + lr
+    float colB = halves_min2(cminB[0], cminB[1]);
     {
-      const float sendA = lh ? cminA[0] : cminA[1], keepA = lh ? cminA[1] : cminA[0];
-      const float sendB = lh ? cminB[0] : cminB[1], keepB = lh ? cminB[1] : cminB[0];
-      cminA[0] = nmin(keepA, __shfl_xor(sendA, 32, kWave));
-      cminB[0] = nmin(keepB, __shfl_xor(sendB, 32, kWave));
+      const bool colInB = wc0 + lh * 32 + lr >= csplit;
+      if (colInB ? mAB : mAA) colA = inf;
+      if (colInB ? mBB : mBA) colB = inf;
     }
     // row minima over this wave's 64 columns, per column segment: transposing
-    // butterflies as in the single-segment path, one per segment
-    const bool colB0 = s_cimg[wn * 64 + lr] != cA, colB1 = s_cimg[wn * 64 + 32 + lr] != cA;
+    // butterflies as in the single-segment path, two when the boundary falls inside
     float rowminA, rowminB;
-    {
+    if (csplit >= wc0 + 64 || csplit <= wc0) {
       float rv[32];
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-          rv[mb * 16 + v] = nmin(colB0 ? inf : d2[mb][0][v], colB1 ? inf : d2[mb][1][v]);
-      transpose_min32(rv, lr);
-      rowminA = rv[0];
+        for (int v = 0; v < 16; ++v) rv[mb * 16 + v] = nmin(d2[mb][0][v], d2[mb][1][v]);
+      const float m = transpose_min32(rv, lr);
+      const bool inA = csplit > wc0;
+      rowminA = inA ? m : inf;
+      rowminB = inA ? inf : m;
+    } else {
+      const bool colB0 = wc0 + lr >= csplit, colB1 = wc0 + 32 + lr >= csplit;
+      {
+        float rv[32];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            rv[mb * 16 + v] = nmin(colB0 ? inf : d2[mb][0][v], colB1 ? inf : d2[mb][1][v]);
+        rowminA = transpose_min32(rv, lr);
+      }
+      {
+        float rv[32];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            rv[mb * 16 + v] = nmin(colB0 ? d2[mb][0][v] : inf, colB1 ? d2[mb][1][v] : inf);
+        rowminB = transpose_min32(rv, lr);
+      }
     }
+    const int rk = wm * 64 + transposed_row(lr, lh);
     {
-      float rv[32];
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int v = 0; v < 16; ++v)
-          rv[mb * 16 + v] = nmin(colB0 ? d2[mb][0][v] : inf, colB1 ? d2[mb][1][v] : inf);
-      transpose_min32(rv, lr);
-      rowminB = rv[0];
+      const bool rowInB = rk >= rsplit;
+      if (rowInB ? mBA : mAA) rowminA = inf;
+      if (rowInB ? mBB : mAB) rowminB = inf;
     }
     __syncthreads();  // operand buffers are no longer read
     float* s_cminA = smem;            // [2 (wm)][BN]
     float* s_cminB = smem + 2 * BN;
     float* s_rminA = smem + 4 * BN;   // [2 (wn)][BM]
     float* s_rminB = smem + 4 * BN + 2 * BM;
-    s_cminA[wm * BN + wn * 64 + lh * 32 + lr] = cminA[0];
-    s_cminB[wm * BN + wn * 64 + lh * 32 + lr] = cminB[0];
-    const int rk = wm * 64 + (lr >> 4) * 32 + ((lr & 15) >> 2) * 8 + lh * 4 + (lr & 3);
+    s_cminA[wm * BN + wn * 64 + lh * 32 + lr] = colA;
+    s_cminB[wm * BN + wn * 64 + lh * 32 + lr] = colB;
     s_rminA[wn * BM + rk] = rowminA;
     s_rminB[wn * BM + rk] = rowminB;
     __syncthreads();
     if (t < BM) {
       const int r = row0 + t;
       if (r < rows) {
-        // a segment with no pair of different images is exactly +inf (masked): skip
-        // it, also because segment B may be the padding image n
+        // a segment pair with no pair of different images is exactly +inf (masked):
+        // skip it, also because segment B may be the padding image n
         const float a = nmin(s_rminA[t], s_rminA[BM + t]);
         const float b = nmin(s_rminB[t], s_rminB[BM + t]);
         if (a != inf) atomicMin(minbits + (long long)r * n + cA, min_key(a));

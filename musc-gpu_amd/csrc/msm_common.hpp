@@ -102,8 +102,8 @@ __device__ inline double row_sumsq(const float* __restrict__ src, int c, int lan
 // ^ 8; row_half_mirror = lane ^ 7, which flips bit 2 like lane ^ 4 and is an
 // equally valid pairing: a lane keeps the half of its items selected by the bit
 // being resolved, its partner holds the complementary half of the same item set,
-// and the partners met over the five stages still span all 32 lanes); stage 16
-// goes through ds_bpermute.
+// and the partners met over the five stages still span all 32 lanes); stage 16 is
+// the permlane16 swap of transpose_min32.
 template <int kHalf>
 __device__ inline float butterfly_partner(float v) {
   const int x = __builtin_bit_cast(int, v);
@@ -114,9 +114,29 @@ __device__ inline float butterfly_partner(float v) {
   return __shfl_xor(v, kHalf, kWave);
 }
 
+// Minimum across the two 32-lane halves of a wave: the lower half receives the
+// minimum of its and its partner's item0, the upper half that of item1
+// (v_permlane32_swap exchanges VDST's upper half with SRC0's lower half, leaving each
+// lane its own kept item in one register and the partner's in the other).
+__device__ inline float halves_min2(float item0, float item1) {
+  // (__uint_as_float on the elements: clang folds __builtin_bit_cast of the second
+  // element of the returned pair to the first)
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(item0), __float_as_uint(item1), false, false);
+  return nmin(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // rv[0] of lane lr ends with min over the 32 lanes of item k = lr (items = 32
-// values per lane).
+// values per lane).  The first stage (lane ^ 16, 16 exchanges) uses
+// v_permlane16_swap: with rv[q] as VDST and rv[q + 16] as SRC0, the swap of VDST's
+// odd 16-lane rows with SRC0's even rows leaves each lane its own kept item in one
+// register and its partner's copy of that item in the other, so one swap and one
+// minimum replace the select / exchange / select of a shuffle.
 __device__ inline float transpose_min32(float (&rv)[32], int lr) {
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(rv[q]), __float_as_uint(rv[q + 16]), false, false);
+    rv[q] = nmin(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
   auto stage = [&](auto half_c) {
     constexpr int half = decltype(half_c)::value;
     const bool up = (lr & half) != 0;
@@ -127,7 +147,6 @@ __device__ inline float transpose_min32(float (&rv)[32], int lr) {
       rv[q] = nmin(keep, butterfly_partner<half>(send));
     }
   };
-  stage(std::integral_constant<int, 16>{});
   stage(std::integral_constant<int, 8>{});
   stage(std::integral_constant<int, 4>{});
   stage(std::integral_constant<int, 2>{});

@@ -336,11 +336,7 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
     }
     float cm[2];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const float send = lh ? cmin[2 * q] : cmin[2 * q + 1];
-      const float keep = lh ? cmin[2 * q + 1] : cmin[2 * q];
-      cm[q] = nmin(keep, __shfl_xor(send, 32, kWave));
-    }
+    for (int q = 0; q < 2; ++q) cm[q] = halves_min2(cmin[2 * q], cmin[2 * q + 1]);
     // row minima over this wave's 128 columns: in-lane over nb, then the transposing
     // butterfly over the 32 lanes of each half
     float rv[32];
@@ -383,10 +379,8 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
   float cmA[2], cmB[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    const float sendA = lh ? cminA[2 * q] : cminA[2 * q + 1], keepA = lh ? cminA[2 * q + 1] : cminA[2 * q];
-    const float sendB = lh ? cminB[2 * q] : cminB[2 * q + 1], keepB = lh ? cminB[2 * q + 1] : cminB[2 * q];
-    cmA[q] = nmin(keepA, __shfl_xor(sendA, 32, kWave));
-    cmB[q] = nmin(keepB, __shfl_xor(sendB, 32, kWave));
+    cmA[q] = halves_min2(cminA[2 * q], cminA[2 * q + 1]);
+    cmB[q] = halves_min2(cminB[2 * q], cminB[2 * q + 1]);
   }
   bool colB[4];
 #pragma unroll
