@@ -291,7 +291,6 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
   const float inf = __int_as_float(kInfBits);
   const int rA = rimg0, cA = cimg0;
   float d2[2][4][16];
-  bool rowB[2][16];  // row lies in image rA + 1 (two-segment tiles)
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -299,25 +298,16 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
       const int i0 = wm * 64 + mb * 32 + g * 8 + lh * 4;
       const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[i0]);
       const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[i0]);
-      const int4 rim = *reinterpret_cast<const int4*>(&s_rimg[i0]);
       const float rv[4] = {rn.x, rn.y, rn.z, rn.w};
       const float rs[4] = {-2.f * ri.x, -2.f * ri.y, -2.f * ri.z, -2.f * ri.w};
-      const int rimg[4] = {rim.x, rim.y, rim.z, rim.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) rowB[mb][g * 4 + e] = rimg[e] != rA;
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
         const int j = wn * 128 + nb * 32 + lr;
         const float cn = s_cnorm[j];
         const float ci = s_cinv[j];
-        const int cimg = s_cimg[j];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // clamped at 0 by min_key, after the minima: max(., 0) commutes with min
-          const float v = fmaf(rs[e] * ci, acc[mb][nb][g * 4 + e], rv[e] + cn);
-          const bool masked = !simple && (rimg[e] == cimg || rimg[e] == n || cimg == n);
-          d2[mb][nb][g * 4 + e] = masked ? inf : v;
-        }
+        for (int e = 0; e < 4; ++e)  // clamped at 0 by min_key, after the minima
+          d2[mb][nb][g * 4 + e] = fmaf(rs[e] * ci, acc[mb][nb][g * 4 + e], rv[e] + cn);
       }
     }
 
@@ -359,58 +349,105 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
     return;
   }
 
-  // Two image segments per dimension (rows: rA, rA + 1; columns: cA, cA + 1);
-  // same-image and padding pairs are +inf already.
+  // Two image segments per dimension (P >= 256: one boundary at most per tile
+  // dimension).  Tile rows [0, rsplit) are image rA, the rest image rA + 1 or padding;
+  // columns likewise with csplit and cA.  Whether a pair is masked (same image, or
+  // padding) depends only on the two segments, so minima are taken per segment over
+  // the raw distances and a masked segment pair becomes +inf afterwards; a wave whose
+  // rows (or columns) lie in one segment reduces them without per-distance selects.
+  const int rsplit = min(TR, min((rA + 1) * p, rows) - row0);
+  const int csplit = min(TC, min((cA + 1) * p, rows) - col0);
+  const int rBimg = row0 + rsplit < rows ? rA + 1 : n;  // used only when segment B is not empty
+  const int cBimg = col0 + csplit < rows ? cA + 1 : n;
+  const bool mAA = rA == cA, mAB = cBimg == n || rA == cBimg;
+  const bool mBA = rBimg == n || rBimg == cA, mBB = rBimg == n || cBimg == n || rBimg == cBimg;
+  const int wr0 = wm * 64, wc0 = wn * 128;
   float cminA[4], cminB[4];
+  if (rsplit >= wr0 + 64 || rsplit <= wr0) {
+    const bool inA = rsplit > wr0;
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) {
-    float a = inf, b = inf;
+    for (int nb = 0; nb < 4; ++nb) {
+      float m = d2[0][nb][0];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+      for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const float x = d2[mb][nb][v];
-        a = rowB[mb][v] ? a : nmin(a, x);
-        b = rowB[mb][v] ? nmin(b, x) : b;
-      }
-    cminA[nb] = a;
-    cminB[nb] = b;
+        for (int v = 0; v < 16; ++v) m = nmin(m, d2[mb][nb][v]);
+      cminA[nb] = inA ? m : inf;
+      cminB[nb] = inA ? inf : m;
+    }
+  } else {
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      float a = inf, b = inf;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const bool inB = wr0 + mb * 32 + (v >> 2) * 8 + lh * 4 + (v & 3) >= rsplit;
+          a = nmin(a, inB ? inf : d2[mb][nb][v]);
+          b = nmin(b, inB ? d2[mb][nb][v] : inf);
+        }
+      cminA[nb] = a;
+      cminB[nb] = b;
+    }
   }
   float cmA[2], cmB[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    cmA[q] = halves_min2(cminA[2 * q], cminA[2 * q + 1]);
+    cmA[q] = halves_min2(cminA[2 * q], cminA[2 * q + 1]);  // column wc0 + (2q + lh) * 32 + lr
     cmB[q] = halves_min2(cminB[2 * q], cminB[2 * q + 1]);
+    const bool colInB = wc0 + (2 * q + lh) * 32 + lr >= csplit;
+    if (colInB ? mAB : mAA) cmA[q] = inf;
+    if (colInB ? mBB : mBA) cmB[q] = inf;
   }
-  bool colB[4];
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb) colB[nb] = s_cimg[wn * 128 + nb * 32 + lr] != cA;
   float rowminA, rowminB;
-  {
+  if (csplit >= wc0 + 128 || csplit <= wc0) {
     float rv[32];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        float m = inf;
+      for (int v = 0; v < 16; ++v)
+        rv[mb * 16 + v] = nmin(nmin(d2[mb][0][v], d2[mb][1][v]), nmin(d2[mb][2][v], d2[mb][3][v]));
+    const float m = transpose_min32(rv, lr);
+    const bool inA = csplit > wc0;
+    rowminA = inA ? m : inf;
+    rowminB = inA ? inf : m;
+  } else {
+    bool colB[4];
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) m = nmin(m, colB[nb] ? inf : d2[mb][nb][v]);
-        rv[mb * 16 + v] = m;
-      }
-    rowminA = transpose_min32(rv, lr);
+    for (int nb = 0; nb < 4; ++nb) colB[nb] = wc0 + nb * 32 + lr >= csplit;
+    {
+      float rv[32];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          float m = inf;
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb) m = nmin(m, colB[nb] ? inf : d2[mb][nb][v]);
+          rv[mb * 16 + v] = m;
+        }
+      rowminA = transpose_min32(rv, lr);
+    }
+    {
+      float rv[32];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          float m = inf;
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb) m = nmin(m, colB[nb] ? d2[mb][nb][v] : inf);
+          rv[mb * 16 + v] = m;
+        }
+      rowminB = transpose_min32(rv, lr);
+    }
   }
+  const int rk = wm * 64 + transposed_row(lr, lh);
   {
-    float rv[32];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        float m = inf;
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) m = nmin(m, colB[nb] ? d2[mb][nb][v] : inf);
-        rv[mb * 16 + v] = m;
-      }
-    rowminB = transpose_min32(rv, lr);
+    const bool rowInB = rk >= rsplit;
+    if (rowInB ? mBA : mAA) rowminA = inf;
+    if (rowInB ? mBB : mAB) rowminB = inf;
   }
   __syncthreads();  // operand buffers are no longer read
   float* s_cminA = reinterpret_cast<float*>(smem);  // [2 (wm)][TC]
@@ -422,7 +459,6 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
     s_cminA[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = cmA[q];
     s_cminB[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = cmB[q];
   }
-  const int rk = wm * 64 + transposed_row(lr, lh);
   s_rminA[wn * TR + rk] = rowminA;
   s_rminB[wn * TR + rk] = rowminB;
   __syncthreads();
