@@ -124,7 +124,7 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
   __shared__ __attribute__((aligned(16))) float smem[kSplit ? kStageFloats : kSmemFloats];
   __shared__ __attribute__((aligned(16))) float s_rnorm[BM];
   __shared__ __attribute__((aligned(16))) float s_cnorm[BN];
-  __shared__ __attribute__((aligned(16))) float s_rinv[BM];   // row scales (1 unless normalising)
+  __shared__ __attribute__((aligned(16))) float s_rinv[BM];   // -2 x row scale (the scale is 1 unless normalising)
   __shared__ __attribute__((aligned(16))) float s_cinv[BN];
   __shared__ int s_rimg[BM], s_cimg[BN];
 
@@ -144,7 +144,7 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
   if (t < BM) {
     const int r = row0 + t;
     s_rnorm[t] = r < rows ? norms[r] : 0.f;
-    s_rinv[t] = r < rows ? inv[r] : 0.f;
+    s_rinv[t] = r < rows ? -2.f * inv[r] : 0.f;  // exact: a power-of-two factor
     s_rimg[t] = r < rows ? r / p : n;  // n marks "no image" (padding)
   } else {
     const int cc = col0 + (t - BM);
@@ -265,7 +265,7 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
         const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[wm * 64 + mb * 32 + g * 8 + lh * 4]);
         const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[wm * 64 + mb * 32 + g * 8 + lh * 4]);
         const float rv[4] = {rn.x, rn.y, rn.z, rn.w};
-        const float rs[4] = {-2.f * ri.x, -2.f * ri.y, -2.f * ri.z, -2.f * ri.w};
+        const float rs[4] = {ri.x, ri.y, ri.z, ri.w};
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
           const float cn = s_cnorm[wn * 64 + nb * 32 + lr];
@@ -338,7 +338,7 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
         const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[i0]);
         const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[i0]);
         const float rv[4] = {rn.x, rn.y, rn.z, rn.w};
-        const float rs[4] = {-2.f * ri.x, -2.f * ri.y, -2.f * ri.z, -2.f * ri.w};
+        const float rs[4] = {ri.x, ri.y, ri.z, ri.w};
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
           const float cn = s_cnorm[wn * 64 + nb * 32 + lr];
@@ -471,7 +471,7 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
     for (int nb = 0; nb < 2; ++nb) {
       const int j = wn * 64 + nb * 32 + lr;
       const float cn = s_cnorm[j];
-      const float cs = -2.f * s_cinv[j];
+      const float cs = s_cinv[j];
       const int ci = s_cimg[j];
 #pragma unroll
       for (int v = 0; v < 16; ++v) {

@@ -170,7 +170,7 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
     if (t < TR) {
       const int r = row0 + t;
       s_rnorm[t] = r < rows ? norms[r] : 0.f;
-      s_rinv[t] = r < rows ? inv[r] : 0.f;
+      s_rinv[t] = r < rows ? -2.f * inv[r] : 0.f;  // -2 x row scale (exact)
       s_rimg[t] = r < rows ? r / p : n;
     }
   }
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
       const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[i0]);
       const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[i0]);
       const float rv[4] = {rn.x, rn.y, rn.z, rn.w};
-      const float rs[4] = {-2.f * ri.x, -2.f * ri.y, -2.f * ri.z, -2.f * ri.w};
+      const float rs[4] = {ri.x, ri.y, ri.z, ri.w};
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
         const int j = wn * 128 + nb * 32 + lr;
