@@ -206,6 +206,63 @@ def cpu_baseline(tokens_cpu, pools_gpu, scores_gpu, maps_gpu, r_list, image_size
     }
 
 
+def config1_full(seed: int, steps: int, reps: int = 3):
+    """Config 1 (plumbing pool: N=8, one layer, r=1, ranks [0, 2)) timed in full on both sides:
+    the GPU pipeline (inputs resident, HIP-event steps after a warm-up) and the oracle's torch
+    CPU restatement of the original backend over the whole job (LNAMD Unfold path on all 8
+    images, compute_scores_fast for every query image, the epilogue), median of `reps` runs,
+    nothing extrapolated.  Every score, map and image score is checked with the agreement gate."""
+    import statistics
+
+    import torch
+    from musc_hip import agreement, pipeline, synthetic
+    from oracle import epilogue as oe
+    from oracle import lnamd as ol
+    from oracle import msm as om
+
+    n, _, n_tok, c, r_list, image_size, desc = CONFIGS['plumbing']
+    dev = torch.device('cuda:0')
+    tokens_cpu = [synthetic.plumbing_tokens(n, n_tok, c, seed=seed)]
+    tokens = [t.to(dev) for t in tokens_cpu]
+    pipeline.score_pool(tokens, r_list, image_size)
+    torch.cuda.synchronize()
+    evs = []
+    for _ in range(steps):
+        ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        ev[0].record()
+        maps, img = pipeline.score_pool(tokens, r_list, image_size)
+        ev[1].record()
+        evs.append(ev)
+    torch.cuda.synchronize()
+    gpu_ms = sorted(a.elapsed_time(b) for a, b in evs)[steps // 2]
+    scores_gpu = pipeline.msm_all(pipeline.lnamd_pools(tokens, r_list)).cpu()    # (R, L, N, P)
+    cpus = host_cpus()
+    torch.set_num_threads(cpus['usable_cpus'])
+    runs = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            per_r = []
+            for r in r_list:
+                feats = ol.l2_normalise(ol.lnamd_embed(tokens_cpu, r))               # (N, P, 1, C)
+                per_r.append([om.MSM(feats[:, :, 0, :].contiguous())])
+            ref_maps, ref_img = oe.maps_and_scores(per_r, image_size)
+        runs.append(time.perf_counter() - t0)
+    cpu_s = statistics.median(runs)
+    ref_scores = torch.stack([torch.stack(l, 0) for l in per_r], 0)
+    gate = {'msm_scores': agreement.compare_arrays(ref_scores.reshape(-1, ref_scores.shape[-1]),
+                                                   scores_gpu.reshape(-1, scores_gpu.shape[-1])),
+            'maps': agreement.compare_arrays(ref_maps, maps.cpu()),
+            'image_scores': agreement.compare_arrays(ref_img, img.cpu())}
+    gate['pass'] = all(g['pass'] for g in gate.values())
+    return {'workload': desc, 'gpu': {'images_per_s': n / (gpu_ms / 1e3), 'median_ms_per_step': gpu_ms,
+                                      'steps': steps},
+            'cpu': {'images_per_s': n / cpu_s, 'median_s': cpu_s, 'runs_s': runs, 'kind': 'port',
+                    'cores': cpus['usable_cpus'], 'torch_threads': torch.get_num_threads(),
+                    'extrapolated': False},
+            'agreement': gate}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split('\n')[0])
     ap.add_argument('--gpus', type=int, default=1)
@@ -376,6 +433,10 @@ def main() -> int:
             result['value'] = None
             result['value_withheld_reason'] = 'GPU results fail the 2e-5 agreement gate against the oracle sample'
         log('[bench] CPU baseline done')
+        if args.config == 'pool':
+            del pools, scores
+            result['config1_full'] = config1_full(args.seed, args.steps)
+            log('[bench] config 1 timed in full on GPU and CPU')
     print(json.dumps(result), flush=True)
     return 0
 
