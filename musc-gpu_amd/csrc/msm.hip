@@ -34,10 +34,14 @@ namespace msm {
 
 constexpr int BM = 128;          // tile rows (query patches)
 constexpr int BN = 128;          // tile columns (reference patches)
-constexpr int BK = 32;           // K chunk (channels) per pipeline stage
+constexpr int BK = 16;           // K chunk (channels) per pipeline stage: the double-buffered
+                                 // stage is 40 KB of LDS, so three workgroups share a CU
+                                 // (three waves per SIMD cover each other's epilogues and barriers)
 constexpr int PITCH = BK + 4;    // LDS row pitch in floats for staged operands
 constexpr int EPITCH = BN + 1;   // LDS row pitch of the epilogue distance tile
 constexpr int THREADS = 256;     // 4 waves, each owns a 64x64 sub-tile
+constexpr int kRowsPerPass = THREADS / (BK / 4);  // rows one 16-byte load per thread covers
+constexpr int kPasses = BM / kRowsPerPass;         // such loads per thread per staged operand
 
 constexpr int kStageFloats = 2 * (BM + BN) * PITCH;       // double-buffered A and B
 constexpr int kEpiFloats = BM * EPITCH;
@@ -80,14 +84,14 @@ typedef float stage4 __attribute__((ext_vector_type(4)));
 // (kLoad 2, whole chunks through a buffer resource, is in the kernel.)
 template <int kLoad>
 __device__ inline void load_chunk(const float* __restrict__ z, int rows, int c, int row0, int k0,
-                                  stage4 (&reg)[4]) {
+                                  stage4 (&reg)[kPasses]) {
   static_assert(kLoad == 0 || kLoad == 1, "whole-chunk loads are issued by the kernel");
   const int t = threadIdx.x;
   const int lrow = t / (BK / 4);
   const int lk = (t % (BK / 4)) * 4;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = row0 + lrow + 32 * i;
+  for (int i = 0; i < kPasses; ++i) {
+    const int r = row0 + lrow + kRowsPerPass * i;
     const int k = k0 + lk;
     stage4 v = {0.f, 0.f, 0.f, 0.f};
     if (r < rows) {
@@ -105,20 +109,20 @@ __device__ inline void load_chunk(const float* __restrict__ z, int rows, int c, 
   }
 }
 
-__device__ inline void store_chunk(float* __restrict__ dst, const stage4 (&reg)[4]) {
+__device__ inline void store_chunk(float* __restrict__ dst, const stage4 (&reg)[kPasses]) {
   const int t = threadIdx.x;
   const int lrow = t / (BK / 4);
   const int lk = (t % (BK / 4)) * 4;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    *reinterpret_cast<stage4*>(dst + (lrow + 32 * i) * PITCH + lk) = reg[i];
+  for (int i = 0; i < kPasses; ++i)
+    *reinterpret_cast<stage4*>(dst + (lrow + kRowsPerPass * i) * PITCH + lk) = reg[i];
 }
 
 // kSplit (p >= BM): a 128-row or 128-column range holds at most one image boundary,
 // so tiles straddling a boundary reduce in registers too, with two image segments
 // per dimension; otherwise (small p) they go through the LDS epilogue.
 template <int kLoad, bool kSplit>
-__global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
+__global__ __launch_bounds__(THREADS, kSplit ? 3 : 2) void msm_pair_min_kernel(
     const float* __restrict__ z, const float* __restrict__ norms, const float* __restrict__ inv,
     uint32_t* __restrict__ minbits, int rows, int n, int p, int c, int T, long long ntiles) {
   __shared__ __attribute__((aligned(16))) float smem[kSplit ? kStageFloats : kSmemFloats];
@@ -168,7 +172,7 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
   // Stage buffer `b` holds A rows at smem + b*(BM+BN)*PITCH, then B rows.
   constexpr int kStage = (BM + BN) * PITCH;
 
-  stage4 ra0[4], rb0[4], ra1[4], rb1[4];
+  stage4 ra0[kPasses], rb0[kPasses], ra1[kPasses], rb1[kPasses];
   // Whole-chunk loads (kLoad 2) go through a buffer resource over z: the byte offset of
   // each staged row is computed once per tile and the chunk offset is the scalar offset,
   // so the K loop does no address arithmetic (the host takes this path for pools under
@@ -176,19 +180,19 @@ __global__ __launch_bounds__(THREADS, 2) void msm_pair_min_kernel(
   const __amdgpu_buffer_rsrc_t zr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(z), (short)0, (int)(uint32_t)((unsigned long long)rows * (unsigned long long)c * 4ull),
       kBufferFlags);
-  uint32_t voffA[4], voffB[4];
+  uint32_t voffA[kPasses], voffB[kPasses];
   if constexpr (kLoad == 2) {
     const int lrow = t / (BK / 4), lk = (t % (BK / 4)) * 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      voffA[i] = ((uint32_t)min(row0 + lrow + 32 * i, rows - 1) * (uint32_t)c + (uint32_t)lk) * 4u;
-      voffB[i] = ((uint32_t)min(col0 + lrow + 32 * i, rows - 1) * (uint32_t)c + (uint32_t)lk) * 4u;
+    for (int i = 0; i < kPasses; ++i) {
+      voffA[i] = ((uint32_t)min(row0 + lrow + kRowsPerPass * i, rows - 1) * (uint32_t)c + (uint32_t)lk) * 4u;
+      voffB[i] = ((uint32_t)min(col0 + lrow + kRowsPerPass * i, rows - 1) * (uint32_t)c + (uint32_t)lk) * 4u;
     }
   }
-  auto load = [&](bool rowsA, int k0, stage4 (&reg)[4]) {
+  auto load = [&](bool rowsA, int k0, stage4 (&reg)[kPasses]) {
     if constexpr (kLoad == 2) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < kPasses; ++i)
         reg[i] = __builtin_bit_cast(stage4, __builtin_amdgcn_raw_buffer_load_b128(zr, (int)(rowsA ? voffA[i] : voffB[i]),
                                                                                   k0 * 4, 0));
     } else {
