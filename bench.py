@@ -1,12 +1,12 @@
 """Benchmark: MuSc mutual scoring of the default pool on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config pool|super_fast|plumbing]
-                    [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config pool|plumbing]
+                    [--no-cpu-baseline] [--no-split]
 
 One step is one pass of the hot path over the whole synthetic pool, inputs
-resident in HBM: LNAMD for every (layer, radius) with the fused L2
-normalisation, the 12 MSM calls (4 layers x 3 radii) and the epilogue
-(layer/radius means, bilinear upsampling to 518 x 518, image scores).  This is
+resident in HBM: LNAMD for every (layer, radius) (window sums of x - mean), the
+12 MSM calls (4 layers x 3 radii, each row L2-normalised inside MSM) and the
+epilogue (layer/radius means, bilinear upsampling to 518 x 518, image scores).  This is
 N=83 images x 4 layers x 1369 patches x 1024 channels,
 radii 1/3/5, all 83*82 image pairs, trimmed ranks [0, 24).
 
@@ -17,7 +17,11 @@ patch pair's 2C-FLOP dot product counted once), divided by that kernel's
 average duration from torch.cuda (HIP) events recorded around every launch in
 the timed region on the stream it runs on.  The CPU baseline is the oracle's
 restatement of the reference's original torch backend, timed on a bounded
-sample on this host and extrapolated to the whole job.
+sample on this host and extrapolated to the whole job; `config1_full` times
+config 1 in full on both sides, with nothing extrapolated.  The roofline object
+also carries this box's sustained fp32 MFMA rate (a calibration kernel with no
+memory traffic, run after the timed steps): the part's clock differs from box
+to box, and the datasheet peak assumes the highest.
 
 The same step is then timed with the split MSM engine (each fp32 dot product
 formed from three fp16 MFMA products, musc_msm_split_*), reported in
@@ -206,6 +210,31 @@ def cpu_baseline(tokens_cpu, pools_gpu, scores_gpu, maps_gpu, r_list, image_size
     }
 
 
+def sustained_fp32_mfma_tflops(dev, reps: int = 3) -> float:
+    """Median fp32 MFMA rate of musc_calibrate_mfma_f32 on this box (2048 workgroups x 4
+    waves x 64000 independent MFMAs, about 15 ms per launch)."""
+    import ctypes
+
+    import torch
+    from musc_hip import _runtime as rt
+
+    blocks, iters = 2048, 1000
+    out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    flop = ctypes.c_double()
+    lib, s = rt.library(), rt.stream(dev)
+    rates = []
+    for it in range(reps + 1):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        rt.check(lib.musc_calibrate_mfma_f32(out.data_ptr(), blocks, iters, ctypes.byref(flop), s),
+                 'musc_calibrate_mfma_f32')
+        e1.record()
+        torch.cuda.synchronize()
+        if it:
+            rates.append(flop.value / (e0.elapsed_time(e1) / 1e3) / 1e12)
+    return sorted(rates)[len(rates) // 2]
+
+
 def config1_full(seed: int, steps: int, reps: int = 3):
     """Config 1 (plumbing pool: N=8, one layer, r=1, ranks [0, 2)) timed in full on both sides:
     the GPU pipeline (inputs resident, HIP-event steps after a warm-up) and the oracle's torch
@@ -333,6 +362,11 @@ def main() -> int:
     h2d_step_s = time.perf_counter() - t1
     del dev_tokens, pinned
 
+    # This box's sustained fp32 MFMA rate (independent MFMAs, no memory traffic), measured
+    # now, outside the timed region: the clock differs from box to box on this part
+    # (2.07-2.38 GHz seen under the pair kernel), and the datasheet peak assumes 2.4 GHz.
+    box_sustained = sustained_fp32_mfma_tflops(dev)
+
     pair_ms = [a.elapsed_time(b) for a, b in timing['pairs']]
     rank_ms = [a.elapsed_time(b) for a, b in timing['rank']]
     rank_avg_s = sum(rank_ms) / len(rank_ms) / 1e3
@@ -369,7 +403,11 @@ def main() -> int:
                      'frac': achieved_tflops / FP32_MFMA_PEAK_TFLOPS, 'traffic': profiled_traffic(args.config),
                      'traffic_source': 'profiles/msm_lnamd_hbm_traffic_config2.md (rocprofv3 PMC, copy-calibrated)',
                      'flop_per_launch': flop_per_launch, 'avg_launch_ms': pair_avg_s * 1e3,
-                     'launches': len(pair_ms)},
+                     'launches': len(pair_ms),
+                     'box_sustained_tflops': box_sustained,
+                     'frac_of_box_sustained': achieved_tflops / box_sustained,
+                     'box_sustained_source': 'musc_calibrate_mfma_f32: independent v_mfma_f32_32x32x2f32, '
+                                             'no memory traffic, same process, after the timed steps'},
         'kernels': {'lnamd_all_radii': {'bound': 'hbm', 'achieved': lnamd_gbps, 'peak': HBM_PEAK_GBPS,
                                         'unit': 'GB/s', 'frac': lnamd_gbps / HBM_PEAK_GBPS,
                                         'algorithmic_bytes': lnamd_bytes, 'avg_launch_ms': lnamd_avg_s * 1e3,
