@@ -412,7 +412,7 @@ def main() -> int:
                                         'unit': 'GB/s', 'frac': lnamd_gbps / HBM_PEAK_GBPS,
                                         'algorithmic_bytes': lnamd_bytes, 'avg_launch_ms': lnamd_avg_s * 1e3,
                                         'note': 'stats + finalize + stream kernels timed together'},
-                    'rank': {'bound': 'hbm', 'kernel': ('msm_rank_insert_kernel' if int((n - 1) * 0.3) <= 32
+                    'rank': {'bound': 'hbm', 'kernel': ('msm_rank_insert2_kernel' if int((n - 1) * 0.3) <= 32
                                                         else 'msm_rank_select_kernel'), 'achieved': rank_gbps,
                              'peak': HBM_PEAK_GBPS, 'unit': 'GB/s', 'frac': rank_gbps / HBM_PEAK_GBPS,
                              'algorithmic_bytes': rank_bytes, 'avg_launch_ms': rank_avg_s * 1e3,

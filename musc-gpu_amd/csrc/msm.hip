@@ -20,11 +20,12 @@
 //                            with unsigned atomicMin on an order-preserving key
 //                            in which NaN wins (min_key, msm_common.hpp).
 //                            The distance matrix never reaches HBM.
-//   4. msm_rank_*_kernel     one thread per patch ranks the n-1 minima (NaN last)
-//                            and averages the square roots of ranks [a, b): a
-//                            sorted register list of the b smallest (b <= 32), or
-//                            the a-th and b-th smallest by a binary search over
-//                            the key bits.
+//   4. msm_rank_*_kernel     ranks each patch's n-1 minima (NaN last) and averages
+//                            the square roots of ranks [a, b): sorted register
+//                            lists of the b smallest (b <= 32; two lanes per patch,
+//                            merged by a bitonic network), or the a-th and b-th
+//                            smallest by a binary search over the key bits (one
+//                            lane per patch).
 #include <mutex>
 
 #include "msm_common.hpp"
@@ -544,9 +545,9 @@ constexpr uint32_t kNoKey = 0xffffffffu;  // NaN minimum, own image, or padding
 // search over the key bits: the largest t with #{key < t} < k, built from the most
 // significant bit down (32 steps of one compare and one add per key).  A workgroup is
 // one wave of 64 consecutive rows, whose keys are one contiguous range: it is staged
-// in LDS with coalesced 16-byte loads, then lane t reads its row starting at key t % n
-// (the order of a row's keys in registers does not matter), so that lanes whose rows
-// start in the same bank (n a multiple of the bank count) still read distinct banks.
+// in LDS with coalesced 16-byte loads.  Rows start every n words; for even n lane t
+// reads its row starting at key t % n (the order of a row's keys in registers does not
+// matter), so that the 32 lanes of a half-wave read distinct banks (n odd: they do).
 constexpr int kRankRows = 64;
 
 template <int kKeys>
@@ -570,7 +571,7 @@ __global__ __launch_bounds__(kRankRows) void msm_rank_select_kernel(const uint32
   const int self = (int)(row / p);
   const uint32_t* mine = s_rowkeys + t * n;
   uint32_t key[kKeys];
-  int j = t % n;  // image of the key in slot s: (t + s) % n
+  int j = (n & 1) ? 0 : t % n;  // image of the key in slot s: (j0 + s) % n
 #pragma unroll
   for (int s = 0; s < kKeys; ++s) {
     const uint32_t v = mine[j];  // j < n always: every read is in range, none is branched around
@@ -620,50 +621,86 @@ __global__ __launch_bounds__(kRankRows) void msm_rank_select_kernel(const uint32
   scores[row] = (double)(float)((sb - sa) / (double)(b - a));
 }
 
-// Short windows (b <= 32, every BASELINE configuration): one thread per row keeps the
-// kList smallest keys seen so far in an ascending register list; each of the row's n
-// keys is inserted by a min/max pass down the list (2 kList instructions per key,
-// against 64 per register slot for the bit search), and ranks [a, b) are read off the
-// list.  Staging as in msm_rank_select_kernel.
+// Short windows (b <= 32, every BASELINE configuration): ascending register lists of
+// the kList smallest keys, each key inserted by a min/max pass down the list (2 kList
+// instructions per key, against 64 per register slot for the bit search).  Two lanes
+// per row: lane lr of each wave half takes row lr of the workgroup's 32 and half of
+// its keys (lower half the first (n+1)/2 images, upper half the rest) into its own
+// list.  The lower lane then takes its partner's list through v_permlane32_swap, forms
+// C[i] = min(A[i], B[N2-1-i]) over both lists padded to N2 = a power of two >= kList
+// (the N2 smallest of the union, a bitonic sequence: A ascending against B descending),
+// sorts it with a bitonic merge (log2 N2 stages of min/max pairs) and sums ranks [a, b)
+// in ascending order: the same keys in the same order as one list over all n keys.
+// Rows start every n words in LDS; for even n a lane starts at key lr of its half so
+// that the 32 lanes of a half read 32 distinct banks (for odd n they already do).
+constexpr int kRank2Rows = 32;
+
 template <int kList>
-__global__ __launch_bounds__(kRankRows) void msm_rank_insert_kernel(const uint32_t* __restrict__ minbits, int rows,
-                                                                    int n, int p, int a, int b,
-                                                                    double* __restrict__ scores) {
-  extern __shared__ __attribute__((aligned(16))) uint32_t s_rowkeys[];  // kRankRows * n
+__global__ __launch_bounds__(kWave) void msm_rank_insert2_kernel(const uint32_t* __restrict__ minbits, int rows,
+                                                                 int n, int p, int a, int b,
+                                                                 double* __restrict__ scores) {
+  constexpr int N2 = kList <= 8 ? 8 : (kList <= 16 ? 16 : 32);
+  extern __shared__ __attribute__((aligned(16))) uint32_t s_rowkeys[];  // kRank2Rows * n
   const int t = threadIdx.x;
-  const long long row0 = (long long)blockIdx.x * kRankRows;
-  const int nrows = (int)min((long long)kRankRows, rows - row0);
+  const int lr = t & 31, lh = t >> 5;
+  const long long row0 = (long long)blockIdx.x * kRank2Rows;
+  const int nrows = (int)min((long long)kRank2Rows, rows - row0);
   const int count = nrows * n;
   const uint32_t* src = minbits + row0 * n;
+  // row0 * n * 4 bytes is a multiple of 128: 16-byte loads are aligned
   const int n4 = count / 4;
-  for (int i = t; i < n4; i += kRankRows)
-    reinterpret_cast<uint4*>(s_rowkeys)[i] = reinterpret_cast<const uint4*>(src)[i];
-  for (int i = 4 * n4 + t; i < count; i += kRankRows) s_rowkeys[i] = src[i];
+  for (int i = t; i < n4; i += kWave) reinterpret_cast<uint4*>(s_rowkeys)[i] = reinterpret_cast<const uint4*>(src)[i];
+  for (int i = 4 * n4 + t; i < count; i += kWave) s_rowkeys[i] = src[i];
   __syncthreads();
-  if (t >= nrows) return;
-  const long long row = row0 + t;
+  // every lane runs the exchange below; lanes past the last row work on row 0's keys
+  const bool active = lr < nrows;
+  const int rr = active ? lr : 0;
+  const long long row = row0 + rr;
   const int self = (int)(row / p);
-  const uint32_t* mine = s_rowkeys + t * n;
+  const uint32_t* mine = s_rowkeys + rr * n;
+  const int h = (n + 1) / 2;
+  const int first = lh ? h : 0, cnt = lh ? n - h : h;  // cnt >= 1 for n >= 2
   uint32_t list[kList];
 #pragma unroll
   for (int i = 0; i < kList; ++i) list[i] = kNoKey;
-  int j = t % n;  // start at key t % n: see msm_rank_select_kernel
+  int j = first + ((n & 1) ? 0 : rr % cnt);  // distinct banks across the half's lanes
 #pragma unroll 2
-  for (int q = 0; q < n; ++q) {
+  for (int q = 0; q < cnt; ++q) {
     const uint32_t v = mine[j];
-    uint32_t x = j != self ? key_bits(v) : kNoKey;  // the own image inserts nothing
+    uint32_t x = j != self ? key_bits(v) : kNoKey;
 #pragma unroll
     for (int i = 0; i < kList; ++i) {
       const uint32_t lo = min(list[i], x);
       x = max(list[i], x);
       list[i] = lo;
     }
-    j = j + 1 == n ? 0 : j + 1;
+    j = j + 1 == first + cnt ? first : j + 1;
   }
+  // lower lanes: partner's list (the upper lanes' registers reach them through the swap)
+  uint32_t other[kList];
+#pragma unroll
+  for (int i = 0; i < kList; ++i) other[i] = __builtin_amdgcn_permlane32_swap(list[i], list[i], false, false)[1];
+  uint32_t cc[N2];
+#pragma unroll
+  for (int i = 0; i < N2; ++i) {
+    const uint32_t ai = i < kList ? list[i] : kNoKey;
+    const uint32_t bi = N2 - 1 - i < kList ? other[N2 - 1 - i] : kNoKey;
+    cc[i] = min(ai, bi);
+  }
+#pragma unroll
+  for (int s = N2 / 2; s >= 1; s >>= 1)
+#pragma unroll
+    for (int i = 0; i < N2; ++i)
+      if ((i & s) == 0) {
+        const uint32_t x = cc[i], y = cc[i + s];
+        cc[i] = min(x, y);
+        cc[i + s] = max(x, y);
+      }
+  if (lh || !active) return;
   double sum = 0.0;
 #pragma unroll
   for (int i = 0; i < kList; ++i)
-    if (i >= a && i < b) sum += (double)sqrtf(__uint_as_float(list[i]));
+    if (i >= a && i < b) sum += (double)sqrtf(__uint_as_float(cc[i]));
   scores[row] = (double)(float)(sum / (double)(b - a));
 }
 
@@ -757,10 +794,10 @@ inline int run_pairs(const float* z, int n, int p, int c, const Workspace& w, hi
 int run_rank(int n, int p, int a, int b, double* scores, const Workspace& w, hipStream_t s) {
   const long long rows = (long long)n * p;
   if (n <= kMaxSelectKeys && b <= 32) {
-    const dim3 grid((unsigned)((rows + kRankRows - 1) / kRankRows)), block(kRankRows);
-    const size_t smem = (size_t)kRankRows * n * sizeof(uint32_t);  // <= 48 KB
+    const dim3 grid((unsigned)((rows + kRank2Rows - 1) / kRank2Rows)), block(kWave);
+    const size_t smem = (size_t)kRank2Rows * n * sizeof(uint32_t);  // <= 24 KB
 #define MUSC_RANK_INSERT(K) \
-  hipLaunchKernelGGL(msm_rank_insert_kernel<K>, grid, block, smem, s, w.minbits, (int)rows, n, p, a, b, scores)
+  hipLaunchKernelGGL(msm_rank_insert2_kernel<K>, grid, block, smem, s, w.minbits, (int)rows, n, p, a, b, scores)
     if (b <= 8) MUSC_RANK_INSERT(8);
     else if (b <= 16) MUSC_RANK_INSERT(16);
     else if (b <= 24) MUSC_RANK_INSERT(24);
