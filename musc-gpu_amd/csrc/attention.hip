@@ -274,8 +274,9 @@ __global__ __launch_bounds__(WAVES * kWave, 3) void attn_fwd_kernel(const float*
 // P V, which is exactly where register 8m + j of the S^T tile holds that key.
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef short short4v __attribute__((ext_vector_type(4)));
 constexpr int KP16 = D + 8;        // K block pitch (halves): 144 B rows
-constexpr int VP16 = KB + 4;       // V^T block pitch (halves): 72 B rows
+constexpr int VR16 = D + 8;        // V block pitch (halves), row-major: 144 B rows
 
 __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Float16* __restrict__ qg,
                                                                      const _Float16* __restrict__ kg,
@@ -284,7 +285,7 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
                                                                      float scale_log2, HeadLayout in,
                                                                      HeadLayout out, int nbh) {
   __shared__ __attribute__((aligned(16))) _Float16 Ks[2][KB * KP16];
-  __shared__ __attribute__((aligned(16))) _Float16 Vt[2][D * VP16];
+  __shared__ __attribute__((aligned(16))) _Float16 Vs[2][KB * VR16];
 
   const int2 unit = fwd_unit(t, nbh);
   if (unit.x < 0) return;
@@ -313,40 +314,35 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
     o0[v] = 0.f;
     o1[v] = 0.f;
   }
+  // m_run: running maximum of this lane's query (the same in both halves of the wave);
+  // l_run: this half-wave's share of the probability sum (the halves' shares are added
+  // once, after the key loop)
   float m_run = -INFINITY, l_run = 0.f;
 
   const int nkb = (t + KB - 1) / KB;
   const int tid = threadIdx.x;
-  // staging: thread tid moves K row tid/8, halves 8*(tid%8).. (16 B) and V rows
-  // 2*(tid/16), 2*(tid/16)+1, halves 4*(tid%16).. (8 B each), one block ahead
+  // staging: thread tid moves row tid/8, halves 8*(tid%8).. (16 B) of a K block and of a
+  // V block; both are stored row-major in LDS
   const int skey = tid / 8, sd8 = (tid % 8) * 8;
-  const int kp = tid / 16, dg = tid % 16;
   // loads through a buffer resource based at the block's first key whose extent ends
-  // with the last valid key: keys past t read zeros, offsets are loop-invariant
-  const uint32_t voK = (uint32_t)(((long long)skey * st + sd8) * 2);
-  const uint32_t voV0 = (uint32_t)(((long long)(2 * kp) * st + 4 * dg) * 2);
-  const uint32_t voV1 = (uint32_t)(((long long)(2 * kp + 1) * st + 4 * dg) * 2);
-  auto block_rsrc = [&](const _Float16* src, int kb) {
-    const long long rem = min(t - kb * KB, KB);  // valid keys of the block, >= 1
+  // with the last valid key: keys past t read zeros, offsets are loop-invariant; the
+  // extent of a full block (all KB keys valid) is loop-invariant too
+  const uint32_t vo = (uint32_t)(((long long)skey * st + sd8) * 2);
+  const int full_extent = (int)(((long long)(KB - 1) * st + D) * 2);
+  auto block_rsrc = [&](const _Float16* src, int kb, auto full_c) {
+    const int extent = decltype(full_c)::value ? full_extent
+                                               : (int)(((long long)(min(t - kb * KB, KB) - 1) * st + D) * 2);
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(src + head + (long long)kb * KB * st), (short)0,
-                                             (int)(((rem - 1) * st + D) * 2), kBufferFlags);
+                                             extent, kBufferFlags);
   };
-  auto load_k = [&](int kb) -> half8 {
-    return __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(block_rsrc(kg, kb), (int)voK, 0, 0));
+  auto load_block = [&](const _Float16* src, int kb, auto full_c) -> half8 {
+    return __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(block_rsrc(src, kb, full_c), (int)vo, 0, 0));
   };
-  auto load_v = [&](int kb, int which) -> half4 {
-    return __builtin_bit_cast(half4, __builtin_amdgcn_raw_buffer_load_b64(block_rsrc(vg, kb), (int)(which ? voV1 : voV0),
-                                                                           0, 0));
-  };
-  auto store_k = [&](int buf, half8 kr) { *reinterpret_cast<half8*>(&Ks[buf][skey * KP16 + sd8]) = kr; };
-  auto store_v = [&](int buf, half4 a, half4 b) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-      half2v pr = {a[i], b[i]};
-      *reinterpret_cast<half2v*>(&Vt[buf][(4 * dg + i) * VP16 + 2 * kp]) = pr;
-    }
-  };
+  using Whole = std::integral_constant<bool, true>;
+  using Part = std::integral_constant<bool, false>;
+  auto store_k = [&](int buf, half8 r) { *reinterpret_cast<half8*>(&Ks[buf][skey * KP16 + sd8]) = r; };
+  auto store_v = [&](int buf, half8 r) { *reinterpret_cast<half8*>(&Vs[buf][skey * VR16 + sd8]) = r; };
+
   // S^T of one staged key block (4 MFMAs over d = 64) plus one MFMA that adds -base to
   // every logit: the A operand's k column 0 is 1 for every key, the B operand's k row 0
   // holds -base for every query (this lane's running maximum as of the issue).  The
@@ -354,64 +350,81 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
   // integer of at most 2048 in magnitude (exact in fp16) or 0.
   half8 ones_col = {};
   ones_col[0] = lh == 0 ? (_Float16)1.f : (_Float16)0.f;
-  auto logits = [&](int buf, float base) -> floatx16 {
-    half8 shift_row = {};
-    shift_row[0] = lh == 0 ? (_Float16)(-base) : (_Float16)0.f;
+  // The running maximum is kept an integer while |m_run| <= 2048 (raised to the next
+  // integer, which only lowers the exponentials), so that it is exact as an fp16 base.
+  constexpr float kBaseLimit = 2048.f;
+  // base of the next logits and the B operand of the shift MFMA for it; both change
+  // only where m_run does
+  float cur_base = 0.f;
+  half8 shift_row = {};
+  auto set_base = [&]() {
+    cur_base = fabsf(m_run) <= kBaseLimit ? m_run : 0.f;  // -inf -> 0
+    shift_row[0] = lh == 0 ? (_Float16)(-cur_base) : (_Float16)0.f;
+  };
+  auto read_k = [&](int buf, half8 (&kf)[4]) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) kf[m] = *reinterpret_cast<const half8*>(&Ks[buf][lq * KP16 + 16 * m + 8 * lh]);
+  };
+  auto logits = [&](const half8 (&kf)[4]) -> floatx16 {
     floatx16 r;
 #pragma unroll
     for (int v = 0; v < 16; ++v) r[v] = 0.f;
     r = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones_col, shift_row, r, 0, 0, 0);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const half8 a = *reinterpret_cast<const half8*>(&Ks[buf][lq * KP16 + 16 * m + 8 * lh]);
-      r = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[m], r, 0, 0, 0);
-    }
+    for (int m = 0; m < 4; ++m) r = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[m], qf[m], r, 0, 0, 0);
     return r;
   };
-  // The running maximum is kept an integer while |m_run| <= 2048 (raised to the next
-  // integer, which only lowers the exponentials), so that it is exact as an fp16 base.
-  constexpr float kBaseLimit = 2048.f;
-  auto issue_base = [&]() { return fabsf(m_run) <= kBaseLimit ? m_run : 0.f; };  // -inf -> 0
-
-  // Software-pipelined key loop: step kb issues the logits MFMAs of block kb+1 beside
-  // the softmax of block kb and its P V MFMAs, so each wave has independent matrix
-  // work while its exponentials and conversions run (this kernel has only ~2.75 waves
-  // per SIMD to hide that chain).  LDS holds K one block ahead of V.  Steps alternate
-  // between two logits register sets (no copy per block).
-  half8 kreg = load_k(0);
-  store_k(0, kreg);
-  half4 v0 = load_v(0, 0), v1 = load_v(0, 1);
-  if (nkb > 1) kreg = load_k(1);
-  __syncthreads();
-  float base_a = issue_base(), base_b = 0.f;
-  floatx16 sa = logits(0, base_a), sb;
-
-  // s holds the logits of block kb minus `base`; the next block's go into sn / bn.
-  auto step = [&](int kb, floatx16& s, float base, floatx16& sn, float& bn, auto more_c) {
-    constexpr bool kMore = decltype(more_c)::value;
-    if constexpr (kMore) store_k((kb + 1) & 1, kreg);
-    store_v(kb & 1, v0, v1);
-    if constexpr (kMore) {
-      if (kb + 2 < nkb) kreg = load_k(kb + 2);
-      v0 = load_v(kb + 1, 0);
-      v1 = load_v(kb + 1, 1);
-    }
-    __syncthreads();
-    if constexpr (kMore) {
-      bn = issue_base();
-      sn = logits((kb + 1) & 1, bn);
-    }
-    if constexpr (!kMore) {
-      if ((kb + 1) * KB > t) {  // only the last block is ragged
+  // V^T fragments of block j: vf[2 mm] feeds o0 (d 0..31), vf[2 mm + 1] feeds o1 (d 32..63).
+  // ds_read_b64_tr_b16 transposes within each group of 16 lanes: lane i's element j is
+  // element i % 4 of the 8 bytes that lane 4 j + i / 4 of the group addressed.  With V
+  // row-major in LDS, the lane (r = lq % 16 of its group) that addresses V[key0 + r / 4]
+  // [d0 + 4 (r % 4) ..] hands element j of lane i the value V[key0 + j][d0 + i], which is
+  // the A operand's (row d0 + i, k = j) for key0 = 16 mm + 4 lh (elements 0..3) and
+  // 16 mm + 8 + 4 lh (elements 4..7), d0 = 16 (lq / 16) (+ 32 for o1).
+  const int vrd = (4 * lh + ((lq & 15) >> 2)) * VR16 + 16 * (lq >> 4) + 4 * (lq & 3);
+  auto read_v = [&](int j, half8 (&vf)[4]) {
+    const _Float16* vb = &Vs[j & 1][vrd];
+    auto tr = [&](int off) {
+      typedef __attribute__((address_space(3))) short4v lds_short4v;
+      return __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)(vb + off)));
+    };
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-          if (kb * KB + (v >> 2) * 8 + lh * 4 + (v & 3) >= t) s[v] = -INFINITY;
+    for (int mm = 0; mm < 2; ++mm) {
+#pragma unroll
+      for (int o = 0; o < 2; ++o) {
+        const half4 lo = tr(16 * mm * VR16 + 32 * o), hi = tr((16 * mm + 8) * VR16 + 32 * o);
+        vf[2 * mm + o] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
     }
+  };
+
+  // Three-stage software pipeline over 32-key blocks.  Step kb issues the logits MFMAs
+  // of block kb+2 and the P V MFMAs of block kb and computes the exponentials of block
+  // kb+1 on the VALU: within a step the matrix work waits only for its LDS reads, never
+  // for the exponentials, so a wave keeps MFMAs in flight while its softmax runs (this
+  // kernel has only ~2.75 waves per SIMD to hide latency).  The branchy part of a
+  // block's softmax (block maximum, lazy rescale, re-base: part_a) runs at the end of
+  // the step that issued its logits.  A rescale there also scales the fp16
+  // probabilities of the previous block, whose P V product is still to come (the
+  // factor is a power of two while |m_run| <= 2048, so that scaling is exact); each
+  // block's probability sum enters l_run with its P V product.  Block j's K sits in
+  // Ks[j & 1] from the top of step j - 2, its V in Vs[j & 1] from the top of step j;
+  // every buffer is rewritten two barriers after its last read.
+  typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+  auto part_a = [&](int j, floatx16& s, float base, half8 (&pf_prev)[2], auto check_c) {
+    if (decltype(check_c)::value && (j + 1) * KB > t) {  // only the last block is ragged
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        if (j * KB + (v >> 2) * 8 + lh * 4 + (v & 3) >= t) s[v] = -INFINITY;
+    }
+    // IEEE maximum: NaN-propagating, one v_maximum3_f32 per two logits
     float bmax = s[0];
 #pragma unroll
-    for (int v = 1; v < 16; ++v) bmax = fmaxf(bmax, s[v]);
-    bmax = halves_max(bmax) + base;  // this block's maximum logit
+    for (int v = 1; v < 16; ++v) bmax = __builtin_elementwise_maximum(bmax, s[v]);
+    {
+      const float2 p = swap_halves(bmax);
+      bmax = __builtin_elementwise_maximum(p.x, p.y) + base;  // this block's maximum logit
+    }
     // lazy rescaling (see kLazyLog2)
     if (!__all(bmax <= m_run + kLazyLog2)) {
       float mnew = fmaxf(m_run, bmax);
@@ -423,55 +436,108 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
         o0[v] *= alpha;
         o1[v] *= alpha;
       }
+      const _Float16 ah = (_Float16)alpha;
+      pf_prev[0] *= ah;
+      pf_prev[1] *= ah;
       m_run = mnew;
+      set_base();
     }
     // re-base the logits when the running maximum moved since they were issued (the
-    // first blocks, the rare lazy raises, and every block once |m_run| > 2048)
+    // rescale above, and every block once |m_run| > 2048)
     const float shift = base - m_run;
     if (__any(shift != 0.f)) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) s[v] += shift;
     }
-    half8 pf[2];
+  };
+  auto part_b = [&](const floatx16& s, half8 (&pf)[2]) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) pf[v >> 3][v & 7] = (_Float16)softmax_exp2(s[v]);
-    // the row sum of the fp16 probabilities the P V product uses, two at a time in fp32
-    typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+  };
+  auto pv = [&](const half8 (&vf)[4], const half8 (&pf)[2]) {
+    // this half-wave's share of the row sum of the fp16 probabilities the product uses,
+    // two at a time in fp32
     const half2v ones = {(_Float16)1.f, (_Float16)1.f};
-    float ps0 = 0.f, ps1 = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      ps0 = __builtin_amdgcn_fdot2(half2v{pf[0][2 * i], pf[0][2 * i + 1]}, ones, ps0, false);
-      ps1 = __builtin_amdgcn_fdot2(half2v{pf[1][2 * i], pf[1][2 * i + 1]}, ones, ps1, false);
+      l_run = __builtin_amdgcn_fdot2(half2v{pf[0][2 * i], pf[0][2 * i + 1]}, ones, l_run, false);
+      l_run = __builtin_amdgcn_fdot2(half2v{pf[1][2 * i], pf[1][2 * i + 1]}, ones, l_run, false);
     }
-    l_run += halves_sum(ps0 + ps1);
-    const int vb = kb & 1;
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
-      const half4 a0l = *reinterpret_cast<const half4*>(&Vt[vb][lq * VP16 + 16 * mm + 4 * lh]);
-      const half4 a0h = *reinterpret_cast<const half4*>(&Vt[vb][lq * VP16 + 16 * mm + 8 + 4 * lh]);
-      const half4 a1l = *reinterpret_cast<const half4*>(&Vt[vb][(32 + lq) * VP16 + 16 * mm + 4 * lh]);
-      const half4 a1h = *reinterpret_cast<const half4*>(&Vt[vb][(32 + lq) * VP16 + 16 * mm + 8 + 4 * lh]);
-      const half8 a0 = {a0l[0], a0l[1], a0l[2], a0l[3], a0h[0], a0h[1], a0h[2], a0h[3]};
-      const half8 a1 = {a1l[0], a1l[1], a1l[2], a1l[3], a1h[0], a1h[1], a1h[2], a1h[3]};
-      o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, pf[mm], o0, 0, 0, 0);
-      o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, pf[mm], o1, 0, 0, 0);
+      o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[2 * mm], pf[mm], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[2 * mm + 1], pf[mm], o1, 0, 0, 0);
     }
   };
-  using More = std::integral_constant<bool, true>;
-  using Last = std::integral_constant<bool, false>;
-  int kb = 0;
-  for (; kb + 2 < nkb; kb += 2) {
-    step(kb, sa, base_a, sb, base_b, More{});
-    step(kb + 1, sb, base_b, sa, base_a, More{});
+  using Check = std::integral_constant<bool, true>;
+  using NoCheck = std::integral_constant<bool, false>;
+
+  // prologue: logits of blocks 0 and 1, exponentials of block 0; K(2) and V(0) in the
+  // staging registers
+  half8 kreg = load_block(kg, 0, Part{});
+  store_k(0, kreg);
+  if (nkb > 1) kreg = load_block(kg, 1, Part{});
+  __syncthreads();
+  set_base();
+  float base_a = cur_base, base_b = 0.f;
+  floatx16 sa, sb;
+  {
+    half8 kf[4];
+    read_k(0, kf);
+    sa = logits(kf);
   }
-  if (kb + 1 < nkb) {
-    step(kb, sa, base_a, sb, base_b, More{});
-    step(kb + 1, sb, base_b, sa, base_a, Last{});
-  } else {
-    step(kb, sa, base_a, sb, base_b, Last{});
+  half8 pfa[2] = {}, pfb[2] = {};
+  part_a(0, sa, base_a, pfb, Check{});  // pfb is all zeros here
+  if (nkb > 1) store_k(1, kreg);
+  if (nkb > 2) kreg = load_block(kg, 2, Part{});
+  half8 vreg = load_block(vg, 0, Part{});
+  __syncthreads();
+  if (nkb > 1) {
+    base_b = cur_base;
+    half8 kf[4];
+    read_k(1, kf);
+    sb = logits(kf);
+  }
+  part_b(sa, pfa);
+  if (nkb > 1) part_a(1, sb, base_b, pfa, Check{});
+
+  // step kb: logits of block kb+2 into s_new, P V of block kb with pf_use, exponentials
+  // of block kb+1 (held in s_next) into pf_make.  kFull: every block named exists and
+  // the blocks loaded are full.  Steps alternate between two register sets (no copies).
+  auto step = [&](int kb, floatx16& s_new, float& b_new, const floatx16& s_next, half8 (&pf_use)[2],
+                  half8 (&pf_make)[2], auto full_c) {
+    constexpr bool kFull = decltype(full_c)::value;
+    if (kFull || kb + 2 < nkb) store_k(kb & 1, kreg);
+    store_v(kb & 1, vreg);
+    if (kFull || kb + 3 < nkb) kreg = load_block(kg, kb + 3, std::integral_constant<bool, kFull>{});
+    if (kFull || kb + 1 < nkb) vreg = load_block(vg, kb + 1, std::integral_constant<bool, kFull>{});
+    __syncthreads();
+    half8 kf[4], vf[4];
+    if (kFull || kb + 2 < nkb) read_k(kb & 1, kf);
+    read_v(kb, vf);
+    if (kFull || kb + 2 < nkb) {
+      b_new = cur_base;
+      s_new = logits(kf);
+    }
+    pv(vf, pf_use);
+    if (kFull || kb + 1 < nkb) part_b(s_next, pf_make);
+    if constexpr (kFull) {
+      part_a(kb + 2, s_new, b_new, pf_make, NoCheck{});
+    } else {
+      if (kb + 2 < nkb) part_a(kb + 2, s_new, b_new, pf_make, Check{});
+    }
+  };
+  int kb = 0;
+  for (; kb + 4 < nkb; kb += 2) {
+    step(kb, sa, base_a, sb, pfa, pfb, Whole{});
+    step(kb + 1, sb, base_b, sa, pfb, pfa, Whole{});
+  }
+  for (; kb < nkb; kb += 2) {
+    step(kb, sa, base_a, sb, pfa, pfb, Part{});
+    if (kb + 1 < nkb) step(kb + 1, sb, base_b, sa, pfb, pfa, Part{});
   }
 
+  l_run = halves_sum(l_run);
   if (q < t) {
     const float inv = 1.f / l_run;
 #pragma unroll

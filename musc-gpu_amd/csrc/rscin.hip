@@ -7,6 +7,10 @@
 // kept entries (the row-normalised D^-1 W times s, :12-18), averaged over k_list
 // (:20).  One workgroup per image i: similarities of row i into LDS, each kept
 // set found by rank counting (ties broken by column index), sums in fp64.  The
+// similarities are accumulated in fp64, so the kept set is the one exact arithmetic
+// selects: where two similarities lie closer together than fp32 rounding can
+// resolve, the reference's own fp32 product keeps one or the other depending on its
+// summation order, and no fp32 ordering could reproduce that choice in general.  The
 // min-max normalisation propagates NaN like numpy's min/max (:27): one NaN raw
 // score makes every refined score NaN, as in the reference.
 #include "common.hpp"
@@ -28,7 +32,7 @@ struct KList {
 
 __global__ __launch_bounds__(kThreads) void rscin_kernel(const float* __restrict__ x, const double* __restrict__ raw,
                                                          int n, int d, KList ks, float* __restrict__ out) {
-  extern __shared__ float w[];  // n similarities of row i
+  extern __shared__ double w[];  // n similarities of row i
   __shared__ double red[2][kThreads / kWave];
   __shared__ double s_min, s_max;
   const int i = blockIdx.x, tid = threadIdx.x;
@@ -58,12 +62,12 @@ __global__ __launch_bounds__(kThreads) void rscin_kernel(const float* __restrict
     s_min = a;
     s_max = b;
   }
-  // similarities W[i][j] = x_i . x_j (fp32)
+  // similarities W[i][j] = x_i . x_j (fp64 accumulation of the fp32 tokens)
   const float* xi = x + (long long)i * d;
   for (int j = wave; j < n; j += kThreads / kWave) {
     const float* xj = x + (long long)j * d;
-    float acc = 0.f;
-    for (int c = lane; c < d; c += kWave) acc = fmaf(xi[c], xj[c], acc);
+    double acc = 0.0;
+    for (int c = lane; c < d; c += kWave) acc = fma((double)xi[c], (double)xj[c], acc);
     acc = wave_sum(acc);
     if (lane == 0) w[j] = acc;
   }
@@ -74,16 +78,16 @@ __global__ __launch_bounds__(kThreads) void rscin_kernel(const float* __restrict
     const int k = ks.k[q];
     double num = 0.0, den = 0.0;
     for (int j = tid; j < n; j += kThreads) {
-      const float v = w[j];
+      const double v = w[j];
       int rank = 0;  // entries strictly before j in descending order
       for (int m = 0; m < n; ++m) {
-        const float u = w[m];
+        const double u = w[m];
         rank += (u > v) || (u == v && m < j);
       }
       if (rank < k) {
         const float s01 = (float)((raw[j] - lo) / span);
-        num += (double)v * (double)s01;
-        den += (double)v;
+        num += v * (double)s01;
+        den += v;
       }
     }
     num = wave_sum(num);
@@ -121,7 +125,7 @@ extern "C" int musc_rscin_f32(const float* cls_tokens, const double* image_score
     if (k_list[q] < 1 || k_list[q] > n) return MUSC_ERR_INVALID_ARG;
     ks.k[q] = k_list[q];
   }
-  hipLaunchKernelGGL(rscin::rscin_kernel, dim3(n), dim3(rscin::kThreads), (size_t)n * sizeof(float), stream,
+  hipLaunchKernelGGL(rscin::rscin_kernel, dim3(n), dim3(rscin::kThreads), (size_t)n * sizeof(double), stream,
                      cls_tokens, image_scores, n, d, ks, out);
   return check_launch();
 }

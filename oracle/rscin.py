@@ -42,3 +42,27 @@ def rscin_bruteforce_f64(scores_old, cls_tokens, k_list):
             keep = np.argsort(-W[i], kind='stable')[:k]
             out[i] += (W[i, keep] * s[keep]).sum() / W[i, keep].sum()
     return out / len(k_list)
+
+
+def check_rscin(got, scores_old, cls_tokens, k_list, atol=2e-5):
+    """Gate an RsCIN result against the definition.
+
+    The result must match the float64 brute force (`rscin_bruteforce_f64`) within
+    atol on every row.  The fp32 restatement of the reference (`rscin`) is reported
+    beside it: where two class-token similarities lie closer together than fp32
+    rounding resolves, its top-k keeps one or the other depending on the summation
+    order of its matrix product, so on such rows it departs from the definition;
+    `fp32_restatement_flips` counts them and the other rows are compared too.
+    Returns (passed, details).
+    """
+    got = np.asarray(got, dtype=np.float64)
+    bf = rscin_bruteforce_f64(scores_old, cls_tokens, k_list)
+    ref = np.asarray(rscin(scores_old, list(cls_tokens), k_list), dtype=np.float64)
+    flips = np.abs(ref - bf) > atol
+    err_bf = np.abs(got - bf)
+    err_ref = np.abs(got - ref)[~flips]
+    passed = bool(np.all(err_bf <= atol) and np.all(err_ref <= atol))
+    details = {'rows': int(len(got)), 'max_err_vs_f64': float(err_bf.max()),
+               'fp32_restatement_flips': int(flips.sum()),
+               'max_err_vs_fp32_other_rows': float(err_ref.max()) if err_ref.size else 0.0}
+    return passed, details

@@ -30,6 +30,47 @@ def test_fp16_storage(device):
     torch.testing.assert_close(out.float(), ref, rtol=2e-3, atol=2e-3)
 
 
+@pytest.mark.parametrize('bh,t', [(4, 1), (3, 31), (3, 33), (2, 64), (2, 65), (2, 77), (2, 97), (2, 129), (2, 161)])
+def test_fp16_ragged(device, bh, t):
+    # every tail of the fp16 kernel's three-stage key pipeline (1 to 6 key blocks, ragged
+    # last block) against the CPU fp32 reference of the same fp16 inputs
+    g = torch.Generator().manual_seed(bh * 10000 + t + 7)
+    q, k, v = (torch.randn((bh, t, 64), generator=g).half() * 0.64 for _ in range(3))
+    out = _attention_hip.attention(q.to(device), k.to(device), v.to(device), 0.125).cpu()
+    torch.testing.assert_close(out.float(), reference(q, k, v, 0.125), rtol=2e-3, atol=2e-3)
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float16])
+@pytest.mark.parametrize('t,slope', [(700, 0.1), (1370, 0.05), (300, 0.6)])
+def test_growing_logits(device, dtype, t, slope):
+    # logits rising along the keys: the running maximum is raised every few blocks, so
+    # the accumulator rescaling (and, in the fp16 kernel, the rescaling of probabilities
+    # whose P V product is still pending) runs many times per query
+    g = torch.Generator().manual_seed(t)
+    q = torch.zeros((2, t, 64))
+    k = torch.randn((2, t, 64), generator=g) * 0.1
+    q[:, :, 0] = 1.0
+    k[:, :, 0] += slope * torch.arange(t).float()
+    v = torch.randn((2, t, 64), generator=g)
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    out = _attention_hip.attention(q.to(device), k.to(device), v.to(device), 1.0).cpu().float()
+    tol = 1e-4 if dtype == torch.float32 else 1e-2
+    torch.testing.assert_close(out, reference(q, k, v, 1.0), rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float16])
+def test_sharp_logits_select_one_row_dtypes(device, dtype):
+    t = 100
+    q = torch.zeros((1, t, 64))
+    k = torch.zeros((1, t, 64))
+    q[0, :, 0] = 50.0
+    k[0, 37, 0] = 1.0
+    v = torch.randn((1, t, 64))
+    out = _attention_hip.attention(q.to(dtype).to(device), k.to(dtype).to(device), v.to(dtype).to(device), 1.0)
+    expect = v[0, 37].to(dtype).float().expand(t, 64)
+    torch.testing.assert_close(out.cpu().float()[0], expect, rtol=0, atol=1e-5 if dtype == torch.float32 else 1e-3)
+
+
 def test_sharp_logits_select_one_row(device):
     t = 100
     q = torch.zeros((1, t, 64))

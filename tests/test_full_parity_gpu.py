@@ -144,8 +144,13 @@ def test_config5_end_to_end_both_engines(device):
     # (c) the pipeline's own outputs (fp32 engine) and RsCIN on the class tokens
     _gate(ref_maps, out['maps'].cpu(), 'config5 run_category maps')
     _gate(ref_img, out['image_scores'].cpu(), 'config5 run_category image scores')
+    # RsCIN's top-k neighbour choice is discontinuous: where two similarities are closer
+    # than fp32 rounding can settle, the reference's own choice depends on its summation
+    # order, so such rows may match either the float64 definition or the fp32
+    # restatement (oracle.rscin.check_rscin); every other row must match both
     cls = out['class_tokens'].cpu().numpy()
-    ref_rs = orc.rscin(ref_img.numpy(), list(cls), [1, 2, 3])
-    _gate(ref_rs, out['scores'].cpu(), 'config5 RsCIN (fp32 engine)')
-    rs16 = _RsCIN_hip.RsCIN(imgs_by_engine['split16'], out['class_tokens'], [1, 2, 3])
-    _gate(ref_rs, rs16.cpu(), 'config5 RsCIN (split16 engine)')
+    for what, got in (('fp32 engine', out['scores']),
+                      ('split16 engine', _RsCIN_hip.RsCIN(imgs_by_engine['split16'], out['class_tokens'], [1, 2, 3]))):
+        ok, info = orc.check_rscin(got.cpu().numpy(), ref_img.numpy(), cls, [1, 2, 3], atol=ATOL)
+        print(f'config5 RsCIN ({what}): pass={ok} {info}', flush=True)
+        assert ok, (what, info)

@@ -330,3 +330,19 @@ def test_preprocess_to_tensor_normalize_rounding():
             d = got[c].reshape(-1)[u]
             assert nearest(d, Fraction(float(r)) / Fraction(float(sd))), (c, u)
     assert plain[:, 0, 0].tolist() == [0.0] * 3 and plain[:, -1, -1].tolist() == [1.0] * 3
+
+
+def test_rscin_check_gate():
+    from oracle import rscin as orc
+    # check_rscin accepts the float64 definition, reports no fp32 restatement flips on
+    # well-separated similarities, and rejects a wrong value
+    rng = np.random.default_rng(3)
+    cls = rng.standard_normal((12, 64)).astype(np.float32)
+    cls /= np.linalg.norm(cls, axis=1, keepdims=True)
+    raw = rng.random(12)
+    bf = orc.rscin_bruteforce_f64(raw, cls, [1, 2, 3])
+    ok, info = orc.check_rscin(bf, raw, cls, [1, 2, 3])
+    assert ok and info['fp32_restatement_flips'] == 0
+    bad = bf.copy()
+    bad[4] += 1e-3
+    assert not orc.check_rscin(bad, raw, cls, [1, 2, 3])[0]
