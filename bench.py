@@ -27,6 +27,13 @@ The same step is then timed with the split MSM engine (each fp32 dot product
 formed from three fp16 MFMA products, musc_msm_split_*), reported in
 `split16_engine` with its own fp16-MFMA roofline and its agreement with the
 fp32 engine's maps; `--no-split` skips it.  The headline stays the fp32 engine.
+
+`attention_config4` reports config 4 beside it: the fused ViT-L/14 block attention
+(B=4, H=16, T=1370, d=64) over 24 blocks of seeded inputs, fp32 and fp16 storage,
+timed GPU-paced (every launch queued behind a short spin kernel, so the events
+measure the kernels and not the Python wrapper's per-call overhead), with its
+MFMA roofline and the first and last blocks checked against a float64
+softmax(q k^T / 8) v; `--no-attention` skips it.
 """
 from __future__ import annotations
 
@@ -292,6 +299,55 @@ def config1_full(seed: int, steps: int, reps: int = 3):
             'agreement': gate}
 
 
+def attention_config4(seed: int, iters: int = 3) -> dict:
+    """Config 4: fused block attention, fp32 and fp16 storage, 24 seeded blocks."""
+    import torch
+    from musc_hip import _attention_hip, synthetic
+
+    dev = torch.device('cuda:0')
+    b, h, t, d = 4, 16, 1370, 64
+    scale = d ** -0.5
+    blocks32 = list(synthetic.attention_blocks(24, b, h, t, d, seed=seed, device=dev))
+    flop = 4.0 * b * h * t * t * d
+    out = {'workload': 'config 4: ViT-L/14 block attention, B=4, H=16, T=1370, d=64, 24 blocks',
+           'flop_per_block': flop,
+           'timing': 'GPU-paced: the 24 launches of an iteration queued behind a spin kernel; mean of '
+                     f'{iters} iterations after one warm-up'}
+    for name, dtype, peak, tol in (('fp32', torch.float32, FP32_MFMA_PEAK_TFLOPS, 2e-5),
+                                   ('fp16', torch.float16, FP16_MFMA_PEAK_TFLOPS, 2e-4)):
+        blocks = [tuple(x.to(dtype) for x in qkv) for qkv in blocks32]
+        worst, ok = 0.0, True
+        for q, k, v in (blocks[0], blocks[-1]):
+            o = _attention_hip.attention(q, k, v, scale).double()
+            q64, k64, v64 = q.double(), k.double(), v.double()
+            ref = torch.bmm(torch.softmax(torch.bmm(q64 * scale, k64.transpose(1, 2).contiguous()), -1), v64)
+            err = (o - ref).abs().max().item()
+            worst = max(worst, err)
+            ok = ok and err <= tol + tol * ref.abs().max().item()
+            del o, q64, k64, v64, ref
+        ts = []
+        for it in range(iters + 1):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda._sleep(10_000_000)
+            e0.record()
+            for q, k, v in blocks:
+                _attention_hip.attention(q, k, v, scale)
+            e1.record()
+            torch.cuda.synchronize()
+            if it:
+                ts.append(e0.elapsed_time(e1) / len(blocks))
+        ms = sum(ts) / len(ts)
+        tf = flop / (ms / 1e3) / 1e12
+        out[name] = {'kernel': 'attn_fwd_kernel' if name == 'fp32' else 'attn_fwd_f16_kernel',
+                     'ms_per_block': ms, 'bound': 'mfma', 'achieved': tf, 'peak': peak, 'unit': 'TFLOP/s',
+                     'frac': tf / peak, 'max_abs_err_vs_float64': worst,
+                     'tolerance': f'{tol} + {tol} * max|ref| (first and last block)', 'pass': ok}
+        del blocks
+    del blocks32
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split('\n')[0])
     ap.add_argument('--gpus', type=int, default=1)
@@ -302,6 +358,7 @@ def main() -> int:
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--no-split', action='store_true',
                     help='skip the second measurement with the split (3x fp16 MFMA) MSM engine')
+    ap.add_argument('--no-attention', action='store_true', help='skip the config-4 attention measurement')
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU only: this build has no multi-GPU path (--gpus {args.gpus} requested). '
@@ -456,6 +513,11 @@ def main() -> int:
             sp['value_withheld_reason'] = 'split16 maps or image scores fail the 2e-5 agreement gate'
         log(f'[bench] split16 engine: {args.steps} steps in {sp_elapsed:.3f} s')
         del maps16, img16
+    if not args.no_attention and args.config == 'pool':
+        result['attention_config4'] = attention_config4(args.seed)
+        a4 = result['attention_config4']
+        log(f"[bench] config-4 attention: fp32 {a4['fp32']['achieved']:.1f} TFLOP/s, "
+            f"fp16 {a4['fp16']['achieved']:.1f} TFLOP/s")
     if not args.no_cpu_baseline:
         log('[bench] timing the CPU baseline (oracle restatement, bounded sample) and checking agreement')
         pools = pipeline.lnamd_pools(tokens, r_list)
