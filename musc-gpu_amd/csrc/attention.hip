@@ -12,8 +12,8 @@
 // then in-register reductions plus one cross-half exchange, the rescale of the
 // running output is a per-lane scalar, and the probabilities already sit in the
 // B-operand layout of the second product O^T += V^T P^T, so P never goes through
-// LDS.  K and V^T blocks of 32 keys are staged in LDS and shared by the 4 waves
-// (128 queries) of a workgroup.
+// LDS.  Blocks of 32 keys are staged in LDS and shared by the waves of a workgroup
+// (fp32: 12 waves, 384 queries, one workgroup per CU; fp16: 4 waves, 128 queries).
 #include <hip/hip_fp16.h>
 
 #include <type_traits>
@@ -66,8 +66,9 @@ constexpr int kBufferFlags = 0x00020000;  // buffer resource word 3 for raw byte
 // grid's padding.  Units are numbered head-major, so the query tiles of one head are
 // consecutive logical ids, which xcd_logical_id places on one XCD: that XCD's L2 then
 // serves the head's K and V blocks to all of its query tiles.
+template <int kTile = QW * WAVES>  // queries per workgroup
 __device__ inline int2 fwd_unit(int t, int nbh) {
-  const int nqt = (t + QW * WAVES - 1) / (QW * WAVES);
+  const int nqt = (t + kTile - 1) / kTile;
   const long long u = xcd_logical_id(blockIdx.x, gridDim.x);
   if (u >= (long long)nqt * nbh) return make_int2(-1, 0);
   return make_int2((int)(u / nqt), (int)(u % nqt));
@@ -110,7 +111,12 @@ __device__ inline void store_kv_row(float* __restrict__ Ks, float* __restrict__ 
   Vt[(d4 + 3) * VPITCH + key] = vv.w;
 }
 
-__global__ __launch_bounds__(WAVES * kWave, 3) void attn_fwd_kernel(const float* __restrict__ qg,
+// The fp32 kernel runs one 12-wave workgroup (384 queries, 3 waves per SIMD) per CU
+// rather than three 4-wave ones: the wave arbiter favours the oldest waves, so of three
+// workgroups sharing a CU one finishes first and the last runs its final blocks alone,
+// with too few waves to keep the MFMA pipe busy; the barrier keeps 12 waves in step.
+constexpr int WAVES32 = 12;
+__global__ __launch_bounds__(WAVES32 * kWave, 1) void attn_fwd_kernel(const float* __restrict__ qg,
                                                                  const float* __restrict__ kg,
                                                                  const float* __restrict__ vg,
                                                                  float* __restrict__ og, int t, float scale_log2,
@@ -118,12 +124,14 @@ __global__ __launch_bounds__(WAVES * kWave, 3) void attn_fwd_kernel(const float*
   __shared__ __attribute__((aligned(16))) float Ks[2][KB * KPITCH];
   __shared__ __attribute__((aligned(16))) float Vt[2][D * VPITCH];
 
-  const int2 unit = fwd_unit(t, nbh);
+  const int2 unit = fwd_unit<QW * WAVES32>(t, nbh);
   if (unit.x < 0) return;
   const int bh = unit.x;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int lq = lane & 31, lh = lane >> 5;
-  const int q = unit.y * (QW * WAVES) + wave * QW + lq;
+  const int q = unit.y * (QW * WAVES32) + wave * QW + lq;
+  // waves whose 32 queries all lie past t only stage and synchronise
+  const bool active = unit.y * (QW * WAVES32) + wave * QW < t;
   const long long head = in.base(bh), st = in.st;
 
   // This lane's query row, pre-scaled by scale*log2(e): qr[s][j] = q[8s + 4h + j].
@@ -150,15 +158,15 @@ __global__ __launch_bounds__(WAVES * kWave, 3) void attn_fwd_kernel(const float*
   float m = -INFINITY, l = 0.f;
 
   const int nkb = (t + KB - 1) / KB;
-  // K / V^T staging: thread tid moves elements idx = tid and tid + 256 of each
-  // 32-key block (key idx/16, channels 4*(idx%16)), loaded one block ahead; the LDS
+  // K / V^T staging: threads 0-511 each move element idx = tid of each 32-key block (key
+  // idx/16, channels 4*(idx%16)) of K and of V, loaded one block ahead; the LDS
   // copy is double-buffered, so one barrier per block suffices.  The loads go through
   // a buffer resource based at the block's first key whose extent ends with the last
   // valid key, so a key past t reads zeros and each thread's byte offset within the
   // block is loop-invariant: no address arithmetic or bounds test per block.
-  const int i0 = threadIdx.x, i1 = threadIdx.x + WAVES * kWave;
+  const bool stager = threadIdx.x < KB * D / 4;  // waves 0-7: one float4 of K and one of V each
+  const int i0 = threadIdx.x & (KB * D / 4 - 1);
   const uint32_t vo0 = (uint32_t)(((long long)(i0 / (D / 4)) * st + 4 * (i0 % (D / 4))) * 4);
-  const uint32_t vo1 = (uint32_t)(((long long)(i1 / (D / 4)) * st + 4 * (i1 % (D / 4))) * 4);
   auto block_rsrc = [&](const float* src, int kb) {
     const long long rem = min(t - kb * KB, KB);  // valid keys of the block, >= 1
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(src + head + (long long)kb * KB * st), (short)0,
@@ -167,28 +175,24 @@ __global__ __launch_bounds__(WAVES * kWave, 3) void attn_fwd_kernel(const float*
   auto ldkv = [&](__amdgpu_buffer_rsrc_t r, uint32_t vo) {
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, 0, 0));
   };
-  float4 k0, k1, v0, v1;
-  {
+  float4 k0 = {}, v0 = {};
+  if (stager) {
     const __amdgpu_buffer_rsrc_t rk = block_rsrc(kg, 0), rv = block_rsrc(vg, 0);
     k0 = ldkv(rk, vo0);
-    k1 = ldkv(rk, vo1);
     v0 = ldkv(rv, vo0);
-    v1 = ldkv(rv, vo1);
   }
   for (int kb = 0; kb < nkb; ++kb) {
     const int buf = kb & 1;
-    store_kv_row(Ks[buf], Vt[buf], i0, k0, v0);
-    store_kv_row(Ks[buf], Vt[buf], i1, k1, v1);
-    {
+    if (stager) {
+      store_kv_row(Ks[buf], Vt[buf], i0, k0, v0);
       // the block after the last is loaded again as the last block (never stored)
       const int nb = min(kb + 1, nkb - 1);
       const __amdgpu_buffer_rsrc_t rk = block_rsrc(kg, nb), rv = block_rsrc(vg, nb);
       k0 = ldkv(rk, vo0);
-      k1 = ldkv(rk, vo1);
       v0 = ldkv(rv, vo0);
-      v1 = ldkv(rv, vo1);
     }
     __syncthreads();
+    if (!active) continue;
 
     // S^T (keys x queries), already in log2 units
     floatx16 s;
@@ -746,10 +750,11 @@ int attention_fwd(const void* q, const void* k, const void* v, void* out, int dt
   if ((long long)batch * heads > 65535) return MUSC_ERR_UNSUPPORTED;
   const float scale_log2 = scale * 1.4426950408889634f;
   const int nbh = batch * heads;
-  const long long units = (long long)((t + attn::QW * attn::WAVES - 1) / (attn::QW * attn::WAVES)) * nbh;
+  const int tile = dtype == MUSC_DTYPE_F32 ? attn::QW * attn::WAVES32 : attn::QW * attn::WAVES;
+  const long long units = (long long)((t + tile - 1) / tile) * nbh;
   const dim3 grid((unsigned)align_up((size_t)units, kXcds));
   if (dtype == MUSC_DTYPE_F32)
-    hipLaunchKernelGGL(attn::attn_fwd_kernel, grid, dim3(attn::WAVES * kWave), 0, stream,
+    hipLaunchKernelGGL(attn::attn_fwd_kernel, grid, dim3(attn::WAVES32 * kWave), 0, stream,
                        static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
                        static_cast<float*>(out), t, scale_log2, in, ol, nbh);
   else
