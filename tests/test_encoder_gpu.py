@@ -102,10 +102,11 @@ def test_masked_call_falls_back(device):
 
 
 @pytest.mark.parametrize('dtype', [torch.float32, torch.float16])
-def test_packed_attention_matches_contiguous(device, dtype):
+@pytest.mark.parametrize('t', [1, 33, 300])
+def test_packed_attention_matches_contiguous(device, dtype, t):
     # the strided kernels read (T, B, 3E) in place; same arithmetic as the contiguous entry
     g = torch.Generator().manual_seed(9)
-    t, b, h = 300, 3, 4
+    b, h = 3, 4
     e = 64 * h
     qkv = (torch.randn((t, b, 3 * e), generator=g) * 0.5).to(dtype).to(device)
     parts = qkv.reshape(t, b, 3, h, 64)
