@@ -59,6 +59,27 @@ def test_growing_logits(device, dtype, t, slope):
 
 
 @pytest.mark.parametrize('dtype', [torch.float32, torch.float16])
+def test_huge_logits(device, dtype):
+    # logits near 2400 (about 3460 in log2 units): past the range in which the fp16 kernel
+    # keeps its running maximum an integer and folds it into the logits MFMA, so it issues
+    # the logits unshifted and re-bases every block
+    g = torch.Generator().manual_seed(17)
+    t = 160
+    q = torch.zeros((2, t, 64))
+    q[:, :, 0] = 60.0
+    k = torch.randn((2, t, 64), generator=g) * 0.1
+    k[:, :, 0] += 40.0 + 0.05 * torch.randn((2, t), generator=g)
+    v = torch.randn((2, t, 64), generator=g)
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    out = _attention_hip.attention(q.to(device), k.to(device), v.to(device), 1.0).cpu().double()
+    q64, k64, v64 = (x.double() for x in (q, k, v))
+    ref = torch.softmax(q64 @ k64.transpose(1, 2), -1) @ v64
+    tol = 1e-4 if dtype == torch.float32 else 1e-2
+    assert torch.isfinite(out).all()
+    torch.testing.assert_close(out, ref, rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize('dtype', [torch.float32, torch.float16])
 def test_sharp_logits_select_one_row_dtypes(device, dtype):
     t = 100
     q = torch.zeros((1, t, 64))
