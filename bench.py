@@ -478,46 +478,56 @@ def main() -> int:
         'cpu_baseline': None,
     }
     if not args.no_split and p >= _MSM_hip.SPLIT_MIN_P:
-        # The same step with the split MSM engine (fp32 dot products from three fp16 MFMA
-        # products), reported beside the headline; its maps are compared with the fp32
-        # engine's maps of the timed run above.
-        for w in range(args.warmup):
-            pipeline.score_pool(tokens, r_list, image_size, msm_engine='split16')
-        torch.cuda.synchronize()
-        sp_timing: dict = {}
-        t2 = time.perf_counter()
-        for s_ in range(args.steps):
-            maps16, img16 = pipeline.score_pool(tokens, r_list, image_size, timing=sp_timing, msm_engine='split16')
-        torch.cuda.synchronize()
-        sp_elapsed = time.perf_counter() - t2
-        sp_pair_ms = [a.elapsed_time(b) for a, b in sp_timing['pairs']]
-        sp_pair_s = sum(sp_pair_ms) / len(sp_pair_ms) / 1e3
-        sp_tf = flop_per_launch / sp_pair_s / 1e12
-        result['split16_engine'] = {
-            'value': n * args.steps / sp_elapsed, 'unit': 'images/s', 'ms_per_step': sp_elapsed / args.steps * 1e3,
-            'dtype': 'fp16 MFMA products (hi.hi + hi.lo + lo.hi), fp32 accumulation',
-            'pair_kernel': 'split_pair_kernel', 'avg_launch_ms': sp_pair_s * 1e3, 'launches': len(sp_pair_ms),
-            'fp32_equivalent_tflops': sp_tf,
-            'roofline': {'bound': 'mfma', 'achieved': 3 * sp_tf, 'peak': FP16_MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
-                         'frac': 3 * sp_tf / FP16_MFMA_PEAK_TFLOPS,
-                         'note': 'three fp16 MFMA products per algorithmic fp32 dot product'},
-            'max_abs_diff_maps_vs_fp32_engine': (maps16 - maps).abs().max().item(),
-            'max_abs_diff_image_scores_vs_fp32_engine': (img16 - img).abs().max().item(),
-            'agreement_vs_fp32_engine': {'maps': agreement.compare_arrays(maps, maps16),
-                                         'image_scores': agreement.compare_arrays(img, img16)},
-        }
-        sp = result['split16_engine']
-        if not all(g['pass'] for g in sp['agreement_vs_fp32_engine'].values()):
-            sp['value_withheld'] = sp.pop('value')
-            sp['value'] = None
-            sp['value_withheld_reason'] = 'split16 maps or image scores fail the 2e-5 agreement gate'
-        log(f'[bench] split16 engine: {args.steps} steps in {sp_elapsed:.3f} s')
-        del maps16, img16
+        # optional sections record their error in the JSON line instead of ending the run,
+        # so that the headline is always printed
+        try:
+            # The same step with the split MSM engine (fp32 dot products from three fp16 MFMA
+            # products), reported beside the headline; its maps are compared with the fp32
+            # engine's maps of the timed run above.
+            for w in range(args.warmup):
+                pipeline.score_pool(tokens, r_list, image_size, msm_engine='split16')
+            torch.cuda.synchronize()
+            sp_timing: dict = {}
+            t2 = time.perf_counter()
+            for s_ in range(args.steps):
+                maps16, img16 = pipeline.score_pool(tokens, r_list, image_size, timing=sp_timing, msm_engine='split16')
+            torch.cuda.synchronize()
+            sp_elapsed = time.perf_counter() - t2
+            sp_pair_ms = [a.elapsed_time(b) for a, b in sp_timing['pairs']]
+            sp_pair_s = sum(sp_pair_ms) / len(sp_pair_ms) / 1e3
+            sp_tf = flop_per_launch / sp_pair_s / 1e12
+            result['split16_engine'] = {
+                'value': n * args.steps / sp_elapsed, 'unit': 'images/s', 'ms_per_step': sp_elapsed / args.steps * 1e3,
+                'dtype': 'fp16 MFMA products (hi.hi + hi.lo + lo.hi), fp32 accumulation',
+                'pair_kernel': 'split_pair_kernel', 'avg_launch_ms': sp_pair_s * 1e3, 'launches': len(sp_pair_ms),
+                'fp32_equivalent_tflops': sp_tf,
+                'roofline': {'bound': 'mfma', 'achieved': 3 * sp_tf, 'peak': FP16_MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
+                             'frac': 3 * sp_tf / FP16_MFMA_PEAK_TFLOPS,
+                             'note': 'three fp16 MFMA products per algorithmic fp32 dot product'},
+                'max_abs_diff_maps_vs_fp32_engine': (maps16 - maps).abs().max().item(),
+                'max_abs_diff_image_scores_vs_fp32_engine': (img16 - img).abs().max().item(),
+                'agreement_vs_fp32_engine': {'maps': agreement.compare_arrays(maps, maps16),
+                                             'image_scores': agreement.compare_arrays(img, img16)},
+            }
+            sp = result['split16_engine']
+            if not all(g['pass'] for g in sp['agreement_vs_fp32_engine'].values()):
+                sp['value_withheld'] = sp.pop('value')
+                sp['value'] = None
+                sp['value_withheld_reason'] = 'split16 maps or image scores fail the 2e-5 agreement gate'
+            log(f'[bench] split16 engine: {args.steps} steps in {sp_elapsed:.3f} s')
+            del maps16, img16
+        except Exception as exc:  # noqa: BLE001
+            result['split16_engine'] = {'error': repr(exc)}
+            log(f'[bench] split16 engine failed: {exc!r}')
     if not args.no_attention and args.config == 'pool':
-        result['attention_config4'] = attention_config4(args.seed)
-        a4 = result['attention_config4']
-        log(f"[bench] config-4 attention: fp32 {a4['fp32']['achieved']:.1f} TFLOP/s, "
-            f"fp16 {a4['fp16']['achieved']:.1f} TFLOP/s")
+        try:
+            result['attention_config4'] = attention_config4(args.seed)
+            a4 = result['attention_config4']
+            log(f"[bench] config-4 attention: fp32 {a4['fp32']['achieved']:.1f} TFLOP/s, "
+                f"fp16 {a4['fp16']['achieved']:.1f} TFLOP/s")
+        except Exception as exc:  # noqa: BLE001
+            result['attention_config4'] = {'error': repr(exc)}
+            log(f'[bench] config-4 attention failed: {exc!r}')
     if not args.no_cpu_baseline:
         log('[bench] timing the CPU baseline (oracle restatement, bounded sample) and checking agreement')
         pools = pipeline.lnamd_pools(tokens, r_list)
@@ -535,8 +545,12 @@ def main() -> int:
         log('[bench] CPU baseline done')
         if args.config == 'pool':
             del pools, scores
-            result['config1_full'] = config1_full(args.seed, args.steps)
-            log('[bench] config 1 timed in full on GPU and CPU')
+            try:
+                result['config1_full'] = config1_full(args.seed, args.steps)
+                log('[bench] config 1 timed in full on GPU and CPU')
+            except Exception as exc:  # noqa: BLE001
+                result['config1_full'] = {'error': repr(exc)}
+                log(f'[bench] config 1 in full failed: {exc!r}')
     print(json.dumps(result), flush=True)
     return 0
 
