@@ -35,20 +35,33 @@ def select_backend(requested, device_type, platform=None):
     return requested, None
 
 
+# The one configuration the super_fast preset was validated on, as (section, key, value), and
+# the settings the preset replaces (models/modules/_backend.py:24-33).
+_SUPER_FAST_REQUIRES = (
+    ('models', 'backbone_name', 'ViT-L-14-336'),
+    ('models', 'pretrained', 'openai'),
+    ('datasets', 'img_resize', 518),
+    ('models', 'batch_size', 4),
+    ('datasets', 'divide_num', 1),
+)
+_SUPER_FAST_PRESET = (('models', 'feature_layers', [5]), ('models', 'r_list', [3]))
+_SUPER_FAST_MISMATCH = ('super_fast requires ViT-L-14-336/openai, img_resize=518, '
+                        'batch_size=4 and divide_num=1; use gpu for other configurations')
+
+
 def configure_backend(cfg, device_type, platform=None):
-    """Apply the opt-in super_fast preset only when its accelerated path is available."""
+    """Apply the opt-in super_fast preset only when its accelerated path is available.
+
+    Returns `cfg` itself unless super_fast is selected; then checks every required setting
+    (ValueError with the reference's message on a mismatch) and returns a deep copy with the
+    preset's layer and aggregation-degree lists, leaving `cfg` untouched.
+    """
     requested = cfg['models'].get('inference_backend', 'original')
-    selected, _ = select_backend(requested, device_type, platform)
-    if selected != 'super_fast':
+    if select_backend(requested, device_type, platform)[0] != 'super_fast':
         return cfg
-    models = cfg['models']
-    datasets = cfg['datasets']
-    if (models['backbone_name'] != 'ViT-L-14-336' or models['pretrained'] != 'openai'
-            or datasets['img_resize'] != 518 or models['batch_size'] != 4
-            or datasets['divide_num'] != 1):
-        raise ValueError('super_fast requires ViT-L-14-336/openai, img_resize=518, '
-                         'batch_size=4 and divide_num=1; use gpu for other configurations')
+    if any(cfg[section][key] != value for section, key, value in _SUPER_FAST_REQUIRES):
+        raise ValueError(_SUPER_FAST_MISMATCH)
     result = deepcopy(cfg)
-    result['models']['feature_layers'] = [5]
-    result['models']['r_list'] = [3]
+    for section, key, value in _SUPER_FAST_PRESET:
+        result[section][key] = list(value)
     return result
