@@ -299,7 +299,9 @@ int musc_attention_weights(const void* q, const void* k, int dtype, int batch, i
  * (t, batch, heads*64) layout the out-projection takes, so the head transposes of
  * the reference's math path (torch/nn/functional.py multi_head_attention_forward,
  * called at models/backbone/open_clip/transformer.py:232-234) are not made.
- * Strides in elements, >= 0, multiples of 16 bytes; in_st, out_st >= d. */
+ * Strides in elements, >= 0, multiples of 16 bytes; in_st, out_st >= d; the forward
+ * pass reads 32-row K/V blocks through 32-bit buffer extents, so (31*in_st + d) times
+ * the element size must stay below 2^31 (else MUSC_ERR_UNSUPPORTED). */
 int musc_attention_fwd_strided(const void* q, const void* k, const void* v, void* out,
                                int dtype, int batch, int heads, int t, int d,
                                long long in_sb, long long in_sh, long long in_st,

@@ -748,6 +748,10 @@ int attention_fwd(const void* q, const void* k, const void* v, void* out, int dt
     return MUSC_ERR_INVALID_ARG;
   if (!layout_ok(in, dtype) || !layout_ok(ol, dtype)) return MUSC_ERR_INVALID_ARG;
   if ((long long)batch * heads > 65535) return MUSC_ERR_UNSUPPORTED;
+  // K/V blocks are read through buffer resources whose extent and per-thread offsets are
+  // 32-bit byte counts: a block of KB rows must span less than 2 GiB
+  const long long elem = dtype == MUSC_DTYPE_F32 ? 4 : 2;
+  if (((long long)(attn::KB - 1) * in.st + attn::D) * elem > 0x7fffffffLL) return MUSC_ERR_UNSUPPORTED;
   const float scale_log2 = scale * 1.4426950408889634f;
   const int nbh = batch * heads;
   const int tile = dtype == MUSC_DTYPE_F32 ? attn::QW * attn::WAVES32 : attn::QW * attn::WAVES;

@@ -116,6 +116,13 @@ def test_maps_and_attention_argument_errors(lib):
     assert lib.musc_maps_f64(fake, 1, 1, 2, 500, 13, fake, None, None) == 1003
     assert lib.musc_attention_fwd(fake, fake, fake, fake, 0, 4, 10, 32, 0.125, None) == 1003
     assert lib.musc_attention_fwd(fake, fake, fake, fake, 7, 4, 10, 64, 0.125, None) == 1001
+    # a K/V row stride whose 32-row block spans 2 GiB or more exceeds the 32-bit buffer
+    # extent (31 * 18e6 * 4 and 31 * 36e6 * 2 bytes are both above 2^31); only strides
+    # that are rejected are passed here, so nothing is launched
+    for dtype, st in ((0, 18_000_000), (1, 36_000_000)):
+        assert (31 * st + 64) * (4 if dtype == 0 else 2) > 2**31
+        assert lib.musc_attention_fwd_strided(fake, fake, fake, fake, dtype, 1, 1, 10, 64, 0, 0, st, 0, 0, 64,
+                                              0.125, None) == 1003
 
 
 def test_preprocess_workspace_and_argument_errors(lib):
