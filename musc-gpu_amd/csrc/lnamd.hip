@@ -619,8 +619,8 @@ int lnamd_run(const void* const* tokens, int n_layers, int in_dtype, int batch, 
   if (c % 4 != 0 || c / 4 > 1024) return MUSC_ERR_UNSUPPORTED;
   const int grid_tokens = tokens_per_image - has_cls;
   int side = 0;
-  while ((side + 1) * (side + 1) <= grid_tokens) ++side;
-  if (grid_tokens < 1 || side * side != grid_tokens) return MUSC_ERR_INVALID_ARG;
+  while ((long long)(side + 1) * (side + 1) <= grid_tokens) ++side;
+  if (grid_tokens < 1 || (long long)side * side != grid_tokens) return MUSC_ERR_INVALID_ARG;
   if (pool_side < 0 || pool_side > side) return MUSC_ERR_INVALID_ARG;
   const bool pooled = pool_side > 0 && pool_side < side;
   if (pooled && (flags & MUSC_LNAMD_L2NORM)) return MUSC_ERR_UNSUPPORTED;
@@ -652,6 +652,8 @@ int lnamd_run(const void* const* tokens, int n_layers, int in_dtype, int batch, 
   if ((reinterpret_cast<uintptr_t>(out) & 15) != 0) return MUSC_ERR_INVALID_ARG;
   if (!workspace || workspace_bytes < lnamd::workspace_bytes(batch, n_layers)) return MUSC_ERR_WORKSPACE;
 
+  // every grid below (units x chunks, units x slices <= units x 1024) stays in int
+  if ((long long)batch * n_layers * 1024 > 0x7fffffffLL) return MUSC_ERR_UNSUPPORTED;
   const int units = batch * n_layers;
   double* partials = static_cast<double*>(workspace);
   double* stats = reinterpret_cast<double*>(static_cast<char*>(workspace) +
