@@ -544,40 +544,45 @@ constexpr uint32_t kNoKey = 0xffffffffu;  // NaN minimum, own image, or padding
 // One thread per row, its n keys in registers (n <= kKeys).  t is found by a binary
 // search over the key bits: the largest t with #{key < t} < k, built from the most
 // significant bit down (32 steps of one compare and one add per key).  A workgroup is
-// one wave of 64 consecutive rows, whose keys are one contiguous range: it is staged
-// in LDS with coalesced 16-byte loads.  Rows start every n words; for even n lane t
-// reads its row starting at key t % n (the order of a row's keys in registers does not
-// matter), so that the 32 lanes of a half-wave read distinct banks (n odd: they do).
+// one wave of 64 consecutive rows; their keys pass through LDS in chunks of 32 images
+// (coalesced loads of 32 consecutive words per row, a pitch of 33 words so that each
+// lane reading its own row hits a distinct bank), which keeps the LDS per wave at 8 KB.
 constexpr int kRankRows = 64;
+constexpr int kRankChunk = 32;
 
 template <int kKeys>
 __global__ __launch_bounds__(kRankRows) void msm_rank_select_kernel(const uint32_t* __restrict__ minbits, int rows,
                                                                     int n, int p, int a, int b,
                                                                     double* __restrict__ scores) {
-  extern __shared__ __attribute__((aligned(16))) uint32_t s_rowkeys[];  // kRankRows * n
+  __shared__ uint32_t s_chunk[kRankRows * (kRankChunk + 1)];
   const int t = threadIdx.x;
   const long long row0 = (long long)blockIdx.x * kRankRows;
   const int nrows = (int)min((long long)kRankRows, rows - row0);
-  const int count = nrows * n;  // keys of this workgroup's rows
-  const uint32_t* src = minbits + row0 * n;
-  // row0 * n * 4 bytes is a multiple of 256: 16-byte loads are aligned
-  const int n4 = count / 4;
-  for (int i = t; i < n4; i += kRankRows)
-    reinterpret_cast<uint4*>(s_rowkeys)[i] = reinterpret_cast<const uint4*>(src)[i];
-  for (int i = 4 * n4 + t; i < count; i += kRankRows) s_rowkeys[i] = src[i];
-  __syncthreads();
-  if (t >= nrows) return;
   const long long row = row0 + t;
-  const int self = (int)(row / p);
-  const uint32_t* mine = s_rowkeys + t * n;
+  const int self = t < nrows ? (int)(row / p) : -1;
   uint32_t key[kKeys];
-  int j = (n & 1) ? 0 : t % n;  // image of the key in slot s: (j0 + s) % n
 #pragma unroll
-  for (int s = 0; s < kKeys; ++s) {
-    const uint32_t v = mine[j];  // j < n always: every read is in range, none is branched around
-    key[s] = (s < n && j != self) ? key_bits(v) : kNoKey;
-    j = j + 1 == n ? 0 : j + 1;
+  for (int c0 = 0; c0 < kKeys; c0 += kRankChunk) {
+    // 64 rows x 32 images: lanes 32h .. 32h+31 of step i read row 2i + h
+#pragma unroll 8
+    for (int i = 0; i < kRankRows / 2; ++i) {
+      const int r = 2 * i + (t >> 5), k = t & 31;
+      uint32_t v = kNoKey;
+      if (r < nrows && c0 + k < n) v = minbits[(row0 + r) * n + c0 + k];
+      s_chunk[r * (kRankChunk + 1) + k] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kRankChunk; ++k) {
+      const int j = c0 + k;
+      if (j < kKeys) {
+        const uint32_t v = s_chunk[t * (kRankChunk + 1) + k];
+        key[j] = (j < n && j != self) ? key_bits(v) : kNoKey;
+      }
+    }
+    __syncthreads();
   }
+  if (t >= nrows) return;
   uint32_t ta = 0, tb = 0;  // a-th and b-th smallest keys (ta stays 0 for a = 0)
   if (a == 0) {
 #pragma unroll 1
@@ -807,7 +812,7 @@ int run_rank(int n, int p, int a, int b, double* scores, const Workspace& w, hip
   }
   if (n <= kMaxSelectKeys) {
     const dim3 grid((unsigned)((rows + kRankRows - 1) / kRankRows)), block(kRankRows);
-    const size_t smem = (size_t)kRankRows * n * sizeof(uint32_t);  // <= 48 KB
+    const size_t smem = 0;  // the chunk buffer is static
 #define MUSC_RANK_LAUNCH(K) \
   hipLaunchKernelGGL(msm_rank_select_kernel<K>, grid, block, smem, s, w.minbits, (int)rows, n, p, a, b, scores)
     if (n <= 32) MUSC_RANK_LAUNCH(32);
