@@ -19,7 +19,11 @@
 //   activation_kernel      QuickGELU or erf-GELU on 16-byte vectors.  fp16 keeps
 //                          torch's roundings: QuickGELU rounds 1.702 x, then the
 //                          sigmoid, then the product to fp16, as the three
-//                          separate torch ops do; GELU rounds once.
+//                          separate torch ops do; GELU rounds once.  The fp16
+//                          sigmoid is formed from the hardware exp2 and reciprocal:
+//                          rounded to fp16 it equals torch's expf-and-divide
+//                          sigmoid for every fp16 input (an elementwise function
+//                          of a 16-bit input, checked over all of them).
 #include <hip/hip_fp16.h>
 
 #include "common.hpp"
@@ -154,6 +158,17 @@ __global__ __launch_bounds__(kRowsPerBlock * kWave) void layernorm_rows_kernel(
   }
 }
 
+// e^-t from the hardware exp2 (about 1 ulp, plus the rounding of t log2 e)
+__device__ inline float exp_neg(float t) { return __builtin_amdgcn_exp2f(-t * 1.4426950408889634f); }
+
+// 1 / d for d >= 1 or d = +inf: the hardware reciprocal refined by one Newton step
+__device__ inline float recip_ge1(float d) {
+  float r = __builtin_amdgcn_rcpf(d);
+  const float err = fmaf(-d, r, 1.f);
+  r = fmaf(err, r, r);
+  return d < INFINITY ? r : 0.f;
+}
+
 // n / N vectors, grid-stride.  mode 0: QuickGELU, mode 1: GELU (erf).
 template <int kDtype, int kMode>
 __global__ __launch_bounds__(256) void activation_kernel(const void* __restrict__ x, void* __restrict__ y,
@@ -170,7 +185,9 @@ __global__ __launch_bounds__(256) void activation_kernel(const void* __restrict_
     for (int j = 0; j < N; ++j) {
       if constexpr (kMode == 0) {
         const float t = round_to<kDtype>(as_fp32(1.702f * v[j]));
-        const float sg = round_to<kDtype>(as_fp32(1.f / (1.f + expf(-t))));
+        // fp16: exp2 and reciprocal in hardware (one Newton step); fp32: expf and IEEE division
+        const float sg = round_to<kDtype>(
+            as_fp32(kDtype == MUSC_DTYPE_F16 ? recip_ge1(1.f + exp_neg(t)) : 1.f / (1.f + expf(-t))));
         v[j] = as_fp32(v[j] * sg);
       } else {
         v[j] = as_fp32(0.5f * v[j] * (1.f + erff(v[j] * 0.70710678118654752f)));

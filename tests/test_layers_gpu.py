@@ -113,6 +113,12 @@ def test_quick_gelu_fp16_every_input(device):
     match = (got[fin] == ref[fin]).float().mean().item()
     print(f'QuickGELU fp16: {match:.6f} of {int(fin.sum())} finite inputs bit-identical to torch', flush=True)
     assert torch.equal(got[fin], ref[fin])
+    # the non-finite inputs: +inf -> +inf, -inf -> NaN (-inf * 0), NaN -> NaN, as torch
+    special = torch.tensor([float('inf'), float('-inf'), float('nan')], dtype=torch.float16, device=device)
+    ref_s = special * torch.sigmoid(1.702 * special)
+    got_s = _layers_hip.activation_(torch.cat([special, special.new_zeros(5)]), rt.ACT_QUICK_GELU)[:3]
+    assert torch.equal(torch.isnan(got_s), torch.isnan(ref_s))
+    assert torch.equal(got_s[~torch.isnan(ref_s)], ref_s[~torch.isnan(ref_s)])
 
 
 def test_gelu_fp16_every_input(device):
