@@ -40,6 +40,25 @@ def test_multi_radius_layouts(device, c):
         assert (rb[k] - ref_u).abs().max().item() <= ATOL
 
 
+@pytest.mark.parametrize('side,c', [(20, 64), (7, 100), (1, 8)])
+def test_wide_radii_in_any_order(device, side, c):
+    # the library takes up to four odd radii up to 9 in any order (the output keeps the
+    # caller's order), and any square grid: small grids where the window exceeds the grid
+    g = torch.Generator().manual_seed(side * 1000 + c)
+    feats = [torch.randn((2, side * side + 1, c), generator=g) * 2 + 0.5 for _ in range(3)]
+    radii = [9, 1, 7, 3]
+    dev = [f.to(device) for f in feats]
+    out = _lnamd_hip.lnamd(dev, radii, layout='rbplc').cpu()
+    assert out.shape == (4, 2, side * side, 3, c)
+    normed = _lnamd_hip.lnamd(dev, radii, layout='rbplc', l2norm=True).cpu()
+    for k, r in enumerate(radii):
+        ref = ol.aggregate_direct(feats, r)
+        err = (out[k] - ref).abs().max().item()
+        assert err <= ATOL, f'r={r}: {err}'
+        err = (normed[k] - ol.l2_normalise(ref)).abs().max().item()
+        assert err <= ATOL, f'r={r} (L2): {err}'
+
+
 def test_fused_l2norm(device):
     g = torch.Generator().manual_seed(5)
     feats = [torch.randn((4, 1370, 1024), generator=g) for _ in range(3)]
