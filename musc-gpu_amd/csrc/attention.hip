@@ -700,7 +700,7 @@ __global__ __launch_bounds__(kWave) void attn_weights_kernel(const void* __restr
         const QFrag<kDtype> kf = load_frag<kDtype>(kg, head, st, kb * KB + lq, t, lh);
         const floatx16 s = logits_t<kDtype>(kf, qf);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[r][v] += exp2f(s[v] * scale_log2 - mx) * il;
+        for (int v = 0; v < 16; ++v) acc[r][v] += softmax_exp2(s[v] * scale_log2 - mx) * il;
       }
     }
   }
@@ -791,7 +791,7 @@ int attention_weights(const void* q, const void* k, int dtype, int batch, int he
     hipLaunchKernelGGL((attn::attn_weights_kernel<MUSC_DTYPE_F32, kKR>), dim3(nqb, (nkb + kKR - 1) / kKR, batch),
                        dim3(kWave), 0, stream, q, k, heads, t, scale_log2, in, stats, weights);
   } else {
-    constexpr int kKR = 8;
+    constexpr int kKR = 4;
     hipLaunchKernelGGL(attn::attn_wstats_kernel<MUSC_DTYPE_F16>, sgrid, dim3(kWave), 0, stream, q, k, t, scale_log2,
                        in, stats);
     hipLaunchKernelGGL((attn::attn_weights_kernel<MUSC_DTYPE_F16, kKR>), dim3(nqb, (nkb + kKR - 1) / kKR, batch),
