@@ -531,8 +531,13 @@ __global__ __launch_bounds__(WAVES * kWave) void attn_fwd_f16_kernel(const _Floa
       if (kb + 2 < nkb) part_a(kb + 2, s_new, b_new, pf_make, Check{});
     }
   };
+  // A pair of whole steps loads K blocks kb+3, kb+4 and V blocks kb+1, kb+2 with the
+  // full-block extent and skips the ragged mask on blocks kb+2, kb+3: it runs only while
+  // all of them are full blocks (kb + 4 < t / KB), so a ragged last block always takes
+  // the checked steps below and no load reads past key t - 1.
+  const int nfull = t / KB;
   int kb = 0;
-  for (; kb + 4 < nkb; kb += 2) {
+  for (; kb + 4 < nfull; kb += 2) {
     step(kb, sa, base_a, sb, pfa, pfb, Whole{});
     step(kb + 1, sb, base_b, sa, pfb, pfa, Whole{});
   }

@@ -102,7 +102,7 @@ def test_masked_call_falls_back(device):
 
 
 @pytest.mark.parametrize('dtype', [torch.float32, torch.float16])
-@pytest.mark.parametrize('t', [1, 33, 300])
+@pytest.mark.parametrize('t', [1, 33, 150, 300, 1370])
 def test_packed_attention_matches_contiguous(device, dtype, t):
     # the strided kernels read (T, B, 3E) in place; same arithmetic as the contiguous entry
     g = torch.Generator().manual_seed(9)
