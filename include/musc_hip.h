@@ -62,7 +62,9 @@ const char* musc_target_arch(void);
 /* Workspace needed by musc_msm_scores_f32 / musc_msm_nearest_f32 for a pool of
  * n images x p patches x c channels.  Writes the byte count to *out.
  * Replaces the scratch tensors the reference allocates inside
- * models/modules/_MSM_gpu.py:717-748. */
+ * models/modules/_MSM_gpu.py:717-748.  Every MSM entry point taking a workspace
+ * requires it to start at a 256-byte-aligned address (MUSC_ERR_INVALID_ARG
+ * otherwise); hipMalloc and torch's allocator return such addresses. */
 int musc_msm_workspace_bytes(int n, int p, int c, size_t* out);
 
 /* Mutual scores of a pool.
@@ -112,19 +114,31 @@ int musc_msm_nearest_f32(const float* z, int n, int p, int c, float* nearest,
                                       inside MSM, so an aggregation that writes
                                       unnormalised features needs no extra pass   */
 
-/* The three stages of musc_msm_scores_f32, for callers that time or overlap
+/* The four stages of musc_msm_scores_f32, for callers that time or overlap
  * them separately (same arguments and workspace):
  *   prepare      row norms ||z||^2 (and, with MUSC_MSM_NORMALIZE_ROWS, the row
  *                scales 1/||z||) and the +inf fill of the minima buffer;
  *   pair_minima  fp32-MFMA pairwise distances of every unordered patch pair of
  *                different images, reduced along rows and columns into the
  *                per-(patch, image) minima (the hot kernel);
+ *   refine       exact minima where ||a||^2 + ||b||^2 - 2 a.b cancels: every
+ *                (patch, image) minimum with d^2 <= 32 FLT_EPSILON c (||q||^2 +
+ *                the image's largest ||r||^2) is recomputed over that image's p
+ *                patches by explicit differences, as the reference recomputes
+ *                such pairs (models/modules/_MSM_gpu.py:219-228); with nothing to
+ *                recompute it reads the minima once.  Works on the workspace of
+ *                either engine (the split engine's included) after its
+ *                pair_minima, with the same z;
  *   rank         trimmed rank means of the minima into scores.
- * prepare must precede pair_minima, which must precede rank, on one stream. */
+ * prepare, pair_minima, refine and rank run in that order on one stream
+ * (musc_msm_scores_f32, musc_msm_nearest_f32 and musc_msm_split_scores_f32 run
+ * all four). */
 int musc_msm_prepare_f32(const float* z, int n, int p, int c, int flags,
                          void* workspace, size_t workspace_bytes, hipStream_t stream);
 int musc_msm_pair_minima_f32(const float* z, int n, int p, int c,
                              void* workspace, size_t workspace_bytes, hipStream_t stream);
+int musc_msm_refine_f32(const float* z, int n, int p, int c,
+                        void* workspace, size_t workspace_bytes, hipStream_t stream);
 int musc_msm_rank_f32(int n, int p, int rank_lo, int rank_hi, double* scores,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 

@@ -54,22 +54,28 @@ constexpr int kBufferFlags = 0x00020000;  // buffer resource word 3 for raw byte
 // ---------------------------------------------------------------------------
 // norms[row] = ||z_row||^2 and inv[row] = 1.  With `normalize`, the row is
 // treated as z / ||z|| (the L2 normalisation of models/musc.py:238 applied on the
-// fly): inv[row] = 1 / ||z_row|| and norms[row] = ||z_row||^2 * inv^2.
-__global__ __launch_bounds__(256) void msm_norms_kernel(const float* __restrict__ z, int rows, int c, int normalize,
-                                                        float* __restrict__ norms, float* __restrict__ inv) {
+// fly): inv[row] = 1 / ||z_row|| and norms[row] = ||z_row||^2 * inv^2.  scale[row]
+// (the refinement's row scale) = inv[row].
+__global__ __launch_bounds__(256) void msm_norms_kernel(const float* __restrict__ z, int rows, int c,
+                                                        int normalize, float* __restrict__ norms,
+                                                        float* __restrict__ inv, float* __restrict__ scale) {
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const long long row = (long long)blockIdx.x * (blockDim.x / kWave) + wave;
   if (row >= rows) return;
   const double acc = row_sumsq(z + row * (long long)c, c, lane);
   if (lane == 0) {
+    float nrm, s;
     if (normalize) {
       const double r = 1.0 / sqrt(acc);
-      inv[row] = (float)r;
-      norms[row] = (float)(acc * r * r);
+      s = (float)r;
+      nrm = (float)(acc * r * r);
     } else {
-      inv[row] = 1.f;
-      norms[row] = (float)acc;
+      s = 1.f;
+      nrm = (float)acc;
     }
+    inv[row] = s;
+    scale[row] = s;
+    norms[row] = nrm;
   }
 }
 
@@ -174,27 +180,33 @@ __global__ __launch_bounds__(THREADS, kSplit ? 3 : 2) void msm_pair_min_kernel(
   constexpr int kStage = (BM + BN) * PITCH;
 
   stage4 ra0[kPasses], rb0[kPasses], ra1[kPasses], rb1[kPasses];
-  // Whole-chunk loads (kLoad 2) go through a buffer resource over z: the byte offset of
-  // each staged row is computed once per tile and the chunk offset is the scalar offset,
-  // so the K loop does no address arithmetic (the host takes this path for pools under
-  // 2 GiB).  Padded rows re-read the last row (masked in the epilogue).
-  const __amdgpu_buffer_rsrc_t zr = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(z), (short)0, (int)(uint32_t)((unsigned long long)rows * (unsigned long long)c * 4ull),
-      kBufferFlags);
+  // Whole-chunk loads (kLoad 2) go through two buffer resources, one based at the first
+  // row of the tile's A panel and one at the first row of its B panel (64-bit bases, so
+  // the pool may have any size; 32-bit offsets within a 128-row panel): the byte offset
+  // of each staged row is computed once per tile and the chunk offset is the scalar
+  // offset, so the K loop does no address arithmetic.  Padded rows re-read the panel's
+  // last row (masked in the epilogue); the extents end with the panels' last rows.
+  const __amdgpu_buffer_rsrc_t zrA = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(z + (long long)row0 * c), (short)0,
+      (int)((uint32_t)(rlast - row0 + 1) * (uint32_t)c * 4u), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t zrB = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(z + (long long)col0 * c), (short)0,
+      (int)((uint32_t)(clast - col0 + 1) * (uint32_t)c * 4u), kBufferFlags);
   uint32_t voffA[kPasses], voffB[kPasses];
   if constexpr (kLoad == 2) {
     const int lrow = t / (BK / 4), lk = (t % (BK / 4)) * 4;
 #pragma unroll
     for (int i = 0; i < kPasses; ++i) {
-      voffA[i] = ((uint32_t)min(row0 + lrow + kRowsPerPass * i, rows - 1) * (uint32_t)c + (uint32_t)lk) * 4u;
-      voffB[i] = ((uint32_t)min(col0 + lrow + kRowsPerPass * i, rows - 1) * (uint32_t)c + (uint32_t)lk) * 4u;
+      voffA[i] = ((uint32_t)min(lrow + kRowsPerPass * i, rlast - row0) * (uint32_t)c + (uint32_t)lk) * 4u;
+      voffB[i] = ((uint32_t)min(lrow + kRowsPerPass * i, clast - col0) * (uint32_t)c + (uint32_t)lk) * 4u;
     }
   }
   auto load = [&](bool rowsA, int k0, stage4 (&reg)[kPasses]) {
     if constexpr (kLoad == 2) {
 #pragma unroll
       for (int i = 0; i < kPasses; ++i)
-        reg[i] = __builtin_bit_cast(stage4, __builtin_amdgcn_raw_buffer_load_b128(zr, (int)(rowsA ? voffA[i] : voffB[i]),
+        reg[i] = __builtin_bit_cast(stage4, __builtin_amdgcn_raw_buffer_load_b128(rowsA ? zrA : zrB,
+                                                                                  (int)(rowsA ? voffA[i] : voffB[i]),
                                                                                   k0 * 4, 0));
     } else {
       load_chunk<kLoad>(z, rows, c, rowsA ? row0 : col0, k0, reg);
@@ -755,12 +767,128 @@ __global__ __launch_bounds__(256) void msm_nearest_kernel(const uint32_t* __rest
   }
 }
 
+// ---------------------------------------------------------------------------
+// Cancellation refinement.  The pair kernels form ||a||^2 + ||b||^2 - 2 a.b, whose
+// rounding error is of the order of eps (||a||^2 + ||b||^2) whatever the distance, so
+// a minimum near 0 (a duplicated image, near-duplicate patches) keeps only the square
+// root of that error: a few 1e-4 in d for unit rows.  The reference's accelerated MSM
+// recomputes every pair with d^2 <= 32 eps C (||q||^2 + ||r||^2) by explicit
+// differences (models/modules/_MSM_gpu.py:219-228).  Here one pass over the minima
+// keys flags each (row, image) minimum at or below 32 eps C (norms[row] + the largest
+// norm of the image) -- the same bound with the image's largest norm, so every pair
+// the reference recomputes lies in a flagged (row, image) or cannot be its minimum --
+// and the wave recomputes that minimum over all P patches of the image as
+// sum_c (s_a a_c - s_b b_c)^2 in fp32 (s the row scales: 1 / ||z|| with row
+// normalisation, else 1), accurate to a few ulps of d^2 itself; identical rows give
+// exactly 0.  Above the bound the expanded form's error in d is at most about
+// eps ||.||^2 / (2 d), far below the 2e-5 gate.  A flagged minimum is replaced
+// (stored), not merged: the exact value may lie above the expanded one.  NaN minima
+// (key 0), the own image and +inf (key kMinFill) are left alone.  With nothing
+// flagged the pass reads the keys once (37.7 MB at N = 83, P = 1369).
+// ---------------------------------------------------------------------------
+constexpr int kRefineRows = 16;                 // rows per wave
+constexpr float kRefineEps = 1.192092896e-7f;   // the fp32 machine epsilon of the reference's bound
+
+// Minimum over rows q in [q0, q1) of sum_c (s_row z_row,c - s_q z_q,c)^2, in every lane.
+// The products are rounded before the difference (no contraction), as the
+// reference's normalised features are rounded before cdist, so identical rows give 0.
+__device__ inline float exact_min_sq(const float* __restrict__ z, const float* __restrict__ scale, long long row,
+                                     long long q0, long long q1, int c, int lane) {
+#pragma clang fp contract(off)
+  const float sa = scale[row];
+  const float* a = z + row * (long long)c;
+  float best = __int_as_float(kInfBits);
+  for (long long q = q0; q < q1; q += 4) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float sb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sb[j] = q + j < q1 ? scale[q + j] : 0.f;
+    if ((c & 3) == 0) {
+      for (int k = 4 * lane; k < c; k += 4 * kWave) {
+        const float4 av = *reinterpret_cast<const float4*>(a + k);
+        const float ax = av.x * sa, ay = av.y * sa, az = av.z * sa, aw = av.w * sa;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (q + j < q1) {
+            const float4 bv = *reinterpret_cast<const float4*>(z + (q + j) * (long long)c + k);
+            const float dx = ax - bv.x * sb[j], dy = ay - bv.y * sb[j];
+            const float dz = az - bv.z * sb[j], dw = aw - bv.w * sb[j];
+            acc[j] = fmaf(dx, dx, acc[j]);
+            acc[j] = fmaf(dy, dy, acc[j]);
+            acc[j] = fmaf(dz, dz, acc[j]);
+            acc[j] = fmaf(dw, dw, acc[j]);
+          }
+        }
+      }
+    } else {
+      for (int k = lane; k < c; k += kWave) {
+        const float ax = a[k] * sa;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (q + j < q1) {
+            const float d = ax - z[(q + j) * (long long)c + k] * sb[j];
+            acc[j] = fmaf(d, d, acc[j]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float d2 = wave_sum(acc[j]);
+      if (q + j < q1) best = nmin(best, d2);
+    }
+  }
+  return best;
+}
+
+// One wave per kRefineRows consecutive rows: their keys are read with consecutive
+// lanes on consecutive keys; a ballot collects the flagged ones, which the whole wave
+// then recomputes one at a time.
+__global__ __launch_bounds__(256) void msm_refine_kernel(const float* __restrict__ z, int rows, int n, int p, int c,
+                                                         const float* __restrict__ norms,
+                                                         const float* __restrict__ scale,
+                                                         const uint32_t* __restrict__ imgmax,
+                                                         uint32_t* __restrict__ minbits, float thr) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const long long row0 = ((long long)blockIdx.x * (blockDim.x / kWave) + wave) * kRefineRows;
+  if (row0 >= rows) return;
+  const int nk = (int)min((long long)kRefineRows, rows - row0) * n;  // <= 16 * 4096
+  uint32_t* keys = minbits + row0 * n;
+  for (int base = 0; base < nk; base += kWave) {
+    const int i = base + lane;
+    bool flag = false;
+    if (i < nk) {
+      const uint32_t key = keys[i];
+      if (key != 0u && key < kMinFill) {
+        const float d2 = __uint_as_float(key - 1u);
+        flag = d2 <= thr * (norms[row0 + i / n] + __uint_as_float(imgmax[i % n]));
+      }
+    }
+    unsigned long long mask = __ballot(flag);
+    while (mask) {
+      const int l = __ffsll((unsigned long long)mask) - 1;
+      mask &= mask - 1;
+      const int ii = base + l;
+      const long long row = row0 + ii / n;
+      const int img = ii % n;
+      const long long q0 = (long long)img * p, q1 = min(q0 + p, (long long)rows);
+      const float d2 = exact_min_sq(z, scale, row, q0, q1, c, lane);
+      if (lane == 0) keys[ii] = min_key(d2);
+    }
+  }
+}
+
+// The workspace holds arrays read with 16-byte loads and merged with 4-byte atomics,
+// each at a 256-byte-aligned offset from its start: the start must be 256-byte aligned.
+inline bool ws_aligned(const void* ws) { return (reinterpret_cast<uintptr_t>(ws) & 255) == 0; }
+
 inline int validate(const float* z, int n, int p, int c, void* ws, size_t ws_bytes) {
   if (!z || n < 2 || p < 1 || c < 1) return MUSC_ERR_INVALID_ARG;
   const long long rows = (long long)n * p;
   if (rows > (1LL << 30)) return MUSC_ERR_UNSUPPORTED;
   if (n > 4096) return MUSC_ERR_UNSUPPORTED;  // rank kernel stages n floats per wave in LDS (64 KB)
   if (!ws || ws_bytes < workspace_bytes(n, p)) return MUSC_ERR_WORKSPACE;
+  if (!ws_aligned(ws)) return MUSC_ERR_INVALID_ARG;
   if ((c & 3) == 0 && (reinterpret_cast<uintptr_t>(z) & 15) != 0) return MUSC_ERR_INVALID_ARG;
   return MUSC_OK;
 }
@@ -769,7 +897,8 @@ inline int validate(const float* z, int n, int p, int c, void* ws, size_t ws_byt
 inline void run_prepare(const float* z, int n, int p, int c, int normalize, const Workspace& w, hipStream_t s) {
   const long long rows = (long long)n * p;
   hipLaunchKernelGGL(msm_norms_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, z, (int)rows, c,
-                     normalize, w.norms, w.inv);
+                     normalize, w.norms, w.inv, w.scale);
+  launch_image_max(w.norms, n, p, w.imgmax, s);
   launch_fill_u32(w.minbits, (size_t)rows * n, kMinFill, s);
 }
 
@@ -784,7 +913,9 @@ inline int run_pairs(const float* z, int n, int p, int c, const Workspace& w, hi
   hipLaunchKernelGGL((msm_pair_min_kernel<V4, SPLIT>), dim3((unsigned)grid), dim3(THREADS), 0, s, z, w.norms, w.inv, \
                      w.minbits, (int)rows, n, p, c, (int)T, ntiles)
   const bool split = p >= BM;
-  if (c % (2 * BK) == 0 && (unsigned long long)rows * (unsigned long long)c * 4ull < (1ull << 31)) {
+  // whole-chunk loads: c a multiple of two chunks, and a 128-row panel addressable with
+  // 32-bit offsets (any pool size: the buffer resources are based at each tile's panels)
+  if (c % (2 * BK) == 0 && (unsigned long long)BM * (unsigned long long)c * 4ull < (1ull << 31)) {
     if (split) MUSC_PAIR_LAUNCH(2, true); else MUSC_PAIR_LAUNCH(2, false);
   } else if ((c & 3) == 0) {
     if (split) MUSC_PAIR_LAUNCH(1, true); else MUSC_PAIR_LAUNCH(1, false);
@@ -795,7 +926,16 @@ inline int run_pairs(const float* z, int n, int p, int c, const Workspace& w, hi
   return check_launch();
 }
 
-// Stage 3: trimmed rank means.
+// Stage 3: exact minima where the expanded form cancels (either engine's keys).
+int run_refine(const float* z, int n, int p, int c, const Workspace& w, hipStream_t s) {
+  const long long rows = (long long)n * p;
+  const long long blocks = ((rows + kRefineRows - 1) / kRefineRows + 3) / 4;
+  hipLaunchKernelGGL(msm_refine_kernel, dim3((unsigned)blocks), dim3(256), 0, s, z, (int)rows, n, p, c, w.norms,
+                     w.scale, w.imgmax, w.minbits, 32.f * kRefineEps * (float)c);
+  return check_launch();
+}
+
+// Stage 4: trimmed rank means.
 int run_rank(int n, int p, int a, int b, double* scores, const Workspace& w, hipStream_t s) {
   const long long rows = (long long)n * p;
   if (n <= kMaxSelectKeys && b <= 32) {
@@ -857,11 +997,19 @@ extern "C" int musc_msm_pair_minima_f32(const float* z, int n, int p, int c, voi
   return msm::run_pairs(z, n, p, c, msm::carve(workspace, n, p), stream);
 }
 
+extern "C" int musc_msm_refine_f32(const float* z, int n, int p, int c, void* workspace, size_t workspace_bytes,
+                                   hipStream_t stream) {
+  int rc = msm::validate(z, n, p, c, workspace, workspace_bytes);
+  if (rc) return rc;
+  return msm::run_refine(z, n, p, c, msm::carve(workspace, n, p), stream);
+}
+
 extern "C" int musc_msm_rank_f32(int n, int p, int rank_lo, int rank_hi, double* scores, void* workspace,
                                  size_t workspace_bytes, hipStream_t stream) {
   if (!scores || n < 2 || p < 1 || rank_lo < 0 || rank_lo >= rank_hi || rank_hi > n - 1) return MUSC_ERR_INVALID_ARG;
-  if (n > 4096) return MUSC_ERR_UNSUPPORTED;
+  if (n > 4096 || (long long)n * p > (1LL << 30)) return MUSC_ERR_UNSUPPORTED;
   if (!workspace || workspace_bytes < msm::workspace_bytes(n, p)) return MUSC_ERR_WORKSPACE;
+  if (!msm::ws_aligned(workspace)) return MUSC_ERR_INVALID_ARG;
   return msm::run_rank(n, p, rank_lo, rank_hi, scores, msm::carve(workspace, n, p), stream);
 }
 
@@ -874,6 +1022,8 @@ extern "C" int musc_msm_scores_f32(const float* z, int n, int p, int c, int rank
   const msm::Workspace w = msm::carve(workspace, n, p);
   msm::run_prepare(z, n, p, c, 0, w, stream);
   rc = msm::run_pairs(z, n, p, c, w, stream);
+  if (rc) return rc;
+  rc = msm::run_refine(z, n, p, c, w, stream);
   if (rc) return rc;
   return msm::run_rank(n, p, rank_lo, rank_hi, scores, w, stream);
 }
@@ -922,7 +1072,7 @@ extern "C" int musc_msm_scores_f32_noalloc(const float* z, int n, int p, int c, 
   void* ws = nullptr;
   const int rc = current_scratch(&ws);
   if (rc) return rc;
-  // the minima keys are refilled by every call (prepare); nothing else carries over
+  // every array of the workspace is rewritten by every call (prepare); nothing carries over
   return musc_msm_scores_f32(z, n, p, c, rank_lo, rank_hi, scores, ws, kScratchBytes, stream);
 }
 
@@ -934,6 +1084,8 @@ extern "C" int musc_msm_nearest_f32(const float* z, int n, int p, int c, float* 
   const msm::Workspace w = msm::carve(workspace, n, p);
   msm::run_prepare(z, n, p, c, 0, w, stream);
   rc = msm::run_pairs(z, n, p, c, w, stream);
+  if (rc) return rc;
+  rc = msm::run_refine(z, n, p, c, w, stream);
   if (rc) return rc;
   const size_t count = (size_t)n * p * n;
   const size_t blocks = (count + 255) / 256 < 65536 ? (count + 255) / 256 : 65536;  // grid-stride beyond

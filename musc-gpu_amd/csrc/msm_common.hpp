@@ -160,31 +160,68 @@ __device__ inline int transposed_row(int lr, int lh) {
   return (lr >> 4) * 32 + ((lr & 15) >> 2) * 8 + lh * 4 + (lr & 3);
 }
 
-// Workspace: norms (n*p fp32) | row scales (n*p fp32) | minima keys (n*p x n uint32,
-// see min_key).
+// Workspace: norms (n*p fp32) | epilogue row scales (n*p fp32) | minima keys (n*p x n
+// uint32, see min_key) | exact-distance row scales (n*p fp32: 1 / ||z_row|| when the
+// rows are normalised, else 1) | per-image maximum of norms (n fp32 bits).  The last
+// two serve the cancellation refinement (msm_refine_kernel), the same for both engines.
 struct Workspace {
   float* norms;
   float* inv;
   uint32_t* minbits;
+  float* scale;
+  uint32_t* imgmax;
 };
 
 inline size_t workspace_bytes(long long n, long long p) {
   const long long rows = n * p;
-  return 2 * align_up((size_t)rows * 4, 256) + align_up((size_t)rows * n * 4, 256);
+  return 3 * align_up((size_t)rows * 4, 256) + align_up((size_t)rows * n * 4, 256) + align_up((size_t)n * 4, 256);
 }
 
 inline Workspace carve(void* ws, long long n, long long p) {
   const long long rows = n * p;
+  const size_t vec = align_up((size_t)rows * 4, 256);
   char* base = static_cast<char*>(ws);
   Workspace w;
   w.norms = reinterpret_cast<float*>(base);
-  w.inv = reinterpret_cast<float*>(base + align_up((size_t)rows * 4, 256));
-  w.minbits = reinterpret_cast<uint32_t*>(base + 2 * align_up((size_t)rows * 4, 256));
+  w.inv = reinterpret_cast<float*>(base + vec);
+  w.minbits = reinterpret_cast<uint32_t*>(base + 2 * vec);
+  w.scale = reinterpret_cast<float*>(base + 2 * vec + align_up((size_t)rows * n * 4, 256));
+  w.imgmax = reinterpret_cast<uint32_t*>(base + 3 * vec + align_up((size_t)rows * n * 4, 256));
   return w;
+}
+
+// imgmax[i] = the bits of the largest finite norms[] of image i's p rows (finite only,
+// so that one NaN or infinite row does not disable the refinement of its image's
+// pairs): one workgroup per image, no atomics.
+template <int kUnused = 0>
+__global__ __launch_bounds__(256) void image_max_kernel(const float* __restrict__ norms, int p,
+                                                        uint32_t* __restrict__ imgmax) {
+  __shared__ float part[256 / kWave];
+  const float* src = norms + (long long)blockIdx.x * p;
+  float m = 0.f;
+  for (int q = threadIdx.x; q < p; q += 256) {
+    const float v = src[q];
+    if (v <= 3.402823466e38f) m = fmaxf(m, v);
+  }
+  m = wave_max(m);
+  if (threadIdx.x % kWave == 0) part[threadIdx.x / kWave] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 256 / kWave; ++w) m = fmaxf(m, part[w]);
+    imgmax[blockIdx.x] = __float_as_uint(m);
+  }
+}
+
+inline void launch_image_max(const float* norms, int n, int p, uint32_t* imgmax, hipStream_t s) {
+  hipLaunchKernelGGL(image_max_kernel<0>, dim3((unsigned)n), dim3(256), 0, s, norms, p, imgmax);
 }
 
 // Trimmed rank means over the minima (defined in msm.hip, shared by both engines).
 int run_rank(int n, int p, int a, int b, double* scores, const Workspace& w, hipStream_t s);
+
+// Exact distances for the minima the expanded form cannot resolve (defined in
+// msm.hip, shared by both engines; runs after either pair kernel).
+int run_refine(const float* z, int n, int p, int c, const Workspace& w, hipStream_t s);
 
 }  // namespace msm
 }  // namespace musc

@@ -69,12 +69,13 @@ typedef int int4v __attribute__((ext_vector_type(4)));
 constexpr int kBufferFlags = 0x00020000;     // buffer resource word 3 for raw byte-addressed loads
 
 // ---------------------------------------------------------------------------
-// Prepare: one wave per row.  norms[] exactly as msm_norms_kernel; inv[] holds the
-// epilogue's per-row scale of the split dot product.
+// Prepare: one wave per row.  norms[], scale[] and the image maxima exactly as
+// msm_norms_kernel; inv[] holds the epilogue's per-row scale of the split dot product.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void split_prepare_kernel(const float* __restrict__ z, int rows, int c, int nkb,
                                                             int normalize, float* __restrict__ norms,
-                                                            float* __restrict__ inv, _Float16* __restrict__ hl) {
+                                                            float* __restrict__ inv, float* __restrict__ scale,
+                                                            _Float16* __restrict__ hl) {
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const long long row = (long long)blockIdx.x * (blockDim.x / kWave) + wave;
   if (row >= rows) return;
@@ -82,14 +83,18 @@ __global__ __launch_bounds__(256) void split_prepare_kernel(const float* __restr
   const double acc = row_sumsq(src, c, lane);
   const double unit = ldexp(1.0, -kScaleShift);
   if (lane == 0) {
+    float nrm;
     if (normalize) {
       const double r = 1.0 / sqrt(acc);
-      norms[row] = (float)(acc * r * r);
+      nrm = (float)(acc * r * r);
       inv[row] = (float)unit;
+      scale[row] = (float)r;
     } else {
-      norms[row] = (float)acc;
+      nrm = (float)acc;
       inv[row] = (float)(sqrt(acc) * unit);
+      scale[row] = 1.f;
     }
+    norms[row] = nrm;
   }
   const double sc = acc > 0.0 ? ldexp(1.0 / sqrt(acc), kScaleShift) : 0.0;
   _Float16* dst = hl + row * (long long)nkb * (2 * KB);
@@ -193,27 +198,36 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
   // (A), 128..383 tile columns (B).  Lane l of a load carries row R = R0 + l/4 into
   // LDS position l % 4, i.e. segment (l % 4) ^ ((R >> 2) & 3).  Padded rows re-read
   // the last row (masked in the epilogue).
-  // Addressing: a buffer resource over the split array, one 32-bit byte offset per
-  // load (row base + segment, loop-invariant) and the stage offset as the scalar
-  // offset; offsets past the array read zeros.  The loads are issued from inline
+  // Addressing: two buffer resources, one based at the first row of the A panel and
+  // one at the first row of the B panel (64-bit bases, so the split array may have any
+  // size; each extent ends with its panel's last row), one 32-bit byte offset per load
+  // within its panel (row + segment, loop-invariant) and the stage offset as the scalar
+  // offset.  A load's 16 staged rows lie all in A or all in B (128 = 8 loads of 16
+  // rows), so each load names one resource.  The loads are issued from inline
   // assembly so that the compiler, which cannot tell the ring buffers apart, does
   // not wait for them before reading another buffer; the loop waits for them
   // explicitly.
   const int lrow = lane >> 2;
-  const unsigned long long hl_addr = reinterpret_cast<unsigned long long>(hl);
-  int4v rsrc;
-  rsrc.x = (int)(uint32_t)(hl_addr & 0xffffffffull);
-  rsrc.y = (int)(uint32_t)(hl_addr >> 32);  // base high bits; stride 0
-  rsrc.z = (int)(uint32_t)((long long)rows * nkb * ROWB);
-  rsrc.w = kBufferFlags;
+  auto panel_rsrc = [&](int first, int last) {
+    const unsigned long long addr =
+        reinterpret_cast<unsigned long long>(hl) + (unsigned long long)first * (unsigned long long)(nkb * ROWB);
+    int4v r;
+    r.x = (int)(uint32_t)(addr & 0xffffffffull);
+    r.y = (int)(uint32_t)(addr >> 32);  // base high bits; stride 0
+    r.z = (int)((uint32_t)(last - first + 1) * (uint32_t)(nkb * ROWB));
+    r.w = kBufferFlags;
+    return r;
+  };
+  const int4v rsrcA = panel_rsrc(row0, rlast), rsrcB = panel_rsrc(col0, clast);
   constexpr int kWaveRows = kStageRows / (THREADS / kWave);
+  static_assert(TR % kRowsPerLoad == 0, "a load's staged rows lie in one panel");
   uint32_t voff[kLoads];
 #pragma unroll
   for (int i = 0; i < kLoads; ++i) {
     const int R = wave * kWaveRows + i * kRowsPerLoad + lrow;
-    const int grow = R < TR ? min(row0 + R, rows - 1) : min(col0 + R - TR, rows - 1);
+    const int prow = R < TR ? min(R, rlast - row0) : min(R - TR, clast - col0);
     const int lseg = (lane & 3) ^ ((R >> 2) & 3);
-    voff[i] = (uint32_t)grow * (uint32_t)(nkb * ROWB) + (uint32_t)(lseg * 16);
+    voff[i] = (uint32_t)prow * (uint32_t)(nkb * ROWB) + (uint32_t)(lseg * 16);
   }
   const uint32_t lds0 = (uint32_t)(size_t)(lds_void*)smem;
   auto issue = [&](int kb, int buf) {
@@ -224,9 +238,10 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
       const uint32_t m0 = __builtin_amdgcn_readfirstlane(
           lds0 + (uint32_t)(buf * kStageBytes + (wave * kWaveRows + i * kRowsPerLoad) * ROWB));
       // s_nop: one wait state between the scalar write of M0 and the load that reads it
+      const bool inA = __builtin_amdgcn_readfirstlane(wave * kWaveRows + i * kRowsPerLoad) < TR;  // wave-uniform
       asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                    :
-                   : "s"(m0), "v"(voff[i]), "s"(rsrc), "s"(soff)
+                   : "s"(m0), "v"(voff[i]), "s"(inA ? rsrcA : rsrcB), "s"(soff)
                    : "memory", "m0");
     }
   };
@@ -500,7 +515,8 @@ inline int validate(int n, int p, int c, void* ws, size_t ws_bytes) {
   if (n < 2 || p < 1 || c < 1) return MUSC_ERR_INVALID_ARG;
   const long long rows = (long long)n * p;
   if (rows > (1LL << 30) || n > 4096) return MUSC_ERR_UNSUPPORTED;
-  if (rows * nkb_of(c) * (long long)ROWB > 0xffffffffLL) return MUSC_ERR_UNSUPPORTED;  // 32-bit buffer offsets
+  // 32-bit offsets within a 256-row panel (the buffer resources are based at each tile's panels)
+  if ((long long)TC * nkb_of(c) * ROWB > 0x7fffffffLL) return MUSC_ERR_UNSUPPORTED;
   if (!ws || ws_bytes < workspace_bytes(n, p, c)) return MUSC_ERR_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0) return MUSC_ERR_INVALID_ARG;
   return MUSC_OK;
@@ -510,7 +526,8 @@ inline void run_prepare(const float* z, int n, int p, int c, int normalize, void
   const long long rows = (long long)n * p;
   const Workspace w = carve(ws, n, p);
   hipLaunchKernelGGL(split_prepare_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, z, (int)rows, c,
-                     nkb_of(c), normalize, w.norms, w.inv, split_array(ws, n, p));
+                     nkb_of(c), normalize, w.norms, w.inv, w.scale, split_array(ws, n, p));
+  launch_image_max(w.norms, n, p, w.imgmax, s);
   launch_fill_u32(w.minbits, (size_t)rows * n, kMinFill, s);
 }
 
@@ -568,5 +585,8 @@ extern "C" int musc_msm_split_scores_f32(const float* z, int n, int p, int c, in
   msm::split::run_prepare(z, n, p, c, (flags & MUSC_MSM_NORMALIZE_ROWS) ? 1 : 0, workspace, stream);
   rc = msm::split::run_pairs(n, p, c, workspace, stream);
   if (rc) return rc;
-  return msm::run_rank(n, p, rank_lo, rank_hi, scores, msm::carve(workspace, n, p), stream);
+  const msm::Workspace w = msm::carve(workspace, n, p);
+  rc = msm::run_refine(z, n, p, c, w, stream);
+  if (rc) return rc;
+  return msm::run_rank(n, p, rank_lo, rank_hi, scores, w, stream);
 }

@@ -103,6 +103,7 @@ def MSM(Z: torch.Tensor, device=None, topmin_min: float = 0, topmin_max: float =
                  'musc_msm_prepare_f32')
         rt.check(lib.musc_msm_pair_minima_f32(z.data_ptr(), n, p, c, ws.data_ptr(), ws.numel(), s),
                  'musc_msm_pair_minima_f32')
+        rt.check(lib.musc_msm_refine_f32(z.data_ptr(), n, p, c, ws.data_ptr(), ws.numel(), s), 'musc_msm_refine_f32')
         rt.check(lib.musc_msm_rank_f32(n, p, a, b, scores.data_ptr(), ws.data_ptr(), ws.numel(), s),
                  'musc_msm_rank_f32')
         return scores

@@ -52,6 +52,7 @@ SIGNATURES = {
     'musc_msm_nearest_f32': (_i, [_vp, _i, _i, _i, _vp, _vp, _sz, _vp]),
     'musc_msm_prepare_f32': (_i, [_vp, _i, _i, _i, _i, _vp, _sz, _vp]),
     'musc_msm_pair_minima_f32': (_i, [_vp, _i, _i, _i, _vp, _sz, _vp]),
+    'musc_msm_refine_f32': (_i, [_vp, _i, _i, _i, _vp, _sz, _vp]),
     'musc_msm_rank_f32': (_i, [_i, _i, _i, _i, _vp, _vp, _sz, _vp]),
     'musc_msm_split_workspace_bytes': (_i, [_i, _i, _i, ctypes.POINTER(_sz)]),
     'musc_msm_split_prepare_f32': (_i, [_vp, _i, _i, _i, _i, _vp, _sz, _vp]),

@@ -54,9 +54,9 @@ def bench_msm(args):
     ws = rt.workspace(_MSM_hip.workspace_bytes(n, p, c, engine), dev)
     scores = torch.empty((n, p), dtype=torch.float64, device=dev)
     lib, s = rt.library(), rt.stream(dev)
-    t = {'prepare': [], 'pairs': [], 'rank': []}
+    t = {'prepare': [], 'pairs': [], 'refine': [], 'rank': []}
     for it in range(args.iters + 1):
-        evs = [_events() for _ in range(3)]
+        evs = [_events() for _ in range(4)]
         evs[0][0].record()
         if engine == 'split16':
             rt.check(lib.musc_msm_split_prepare_f32(z.data_ptr(), n, p, c, 0, ws.data_ptr(), ws.numel(), s),
@@ -71,8 +71,11 @@ def bench_msm(args):
             rt.check(lib.musc_msm_pair_minima_f32(z.data_ptr(), n, p, c, ws.data_ptr(), ws.numel(), s), 'pairs')
         evs[1][1].record()
         evs[2][0].record()
-        rt.check(lib.musc_msm_rank_f32(n, p, a, b, scores.data_ptr(), ws.data_ptr(), ws.numel(), s), 'rank')
+        rt.check(lib.musc_msm_refine_f32(z.data_ptr(), n, p, c, ws.data_ptr(), ws.numel(), s), 'refine')
         evs[2][1].record()
+        evs[3][0].record()
+        rt.check(lib.musc_msm_rank_f32(n, p, a, b, scores.data_ptr(), ws.data_ptr(), ws.numel(), s), 'rank')
+        evs[3][1].record()
         torch.cuda.synchronize()
         if it > 0:
             for k, (e0, e1) in zip(t, evs):

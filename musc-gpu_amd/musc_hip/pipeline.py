@@ -89,6 +89,8 @@ def msm_all(pools: torch.Tensor, topmin_min: float = 0, topmin_max: float = 0.3,
                 if pair_events is not None:
                     ev[1].record()
                     pair_events.append(ev)
+                rt.check(lib.musc_msm_refine_f32(z.data_ptr(), n, p, c, ws.data_ptr(), ws.numel(), s),
+                         'musc_msm_refine_f32')
                 if rank_events is not None:
                     rev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                     rev[0].record()

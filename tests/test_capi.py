@@ -48,7 +48,8 @@ def test_msm_workspace_bytes(lib):
     assert lib.musc_msm_workspace_bytes(83, 1369, 1024, ctypes.byref(out)) == 0
     rows = 83 * 1369
     align = lambda x: (x + 255) // 256 * 256  # noqa: E731
-    assert out.value == 2 * align(rows * 4) + align(rows * 83 * 4)
+    # norms | epilogue scales | minima keys | refinement scales | per-image norm maxima
+    assert out.value == 3 * align(rows * 4) + align(rows * 83 * 4) + align(83 * 4)
     assert lib.musc_msm_workspace_bytes(1, 10, 10, ctypes.byref(out)) == 1001
 
 
@@ -88,6 +89,25 @@ def test_msm_argument_errors_before_any_launch(lib):
     assert lib.musc_msm_scores_f32(None, 8, 10, 16, 0, 2, fake, fake, big, None) == 1001
     # more images than the rank kernel stages
     assert lib.musc_msm_scores_f32(fake, 5000, 1, 16, 0, 2, fake, fake, big, None) == 1003
+
+
+def test_msm_workspace_must_be_256_byte_aligned(lib):
+    # every MSM entry point that takes a workspace rejects one that does not start on a
+    # 256-byte boundary (its arrays are read with 16-byte loads and merged with atomics)
+    fake, off = ctypes.c_void_p(256), ctypes.c_void_p(256 + 4)
+    big = ctypes.c_size_t(1 << 40)
+    assert lib.musc_msm_scores_f32(fake, 8, 10, 16, 0, 2, fake, off, big, None) == 1001
+    assert lib.musc_msm_prepare_f32(fake, 8, 10, 16, 0, off, big, None) == 1001
+    assert lib.musc_msm_pair_minima_f32(fake, 8, 10, 16, off, big, None) == 1001
+    assert lib.musc_msm_refine_f32(fake, 8, 10, 16, off, big, None) == 1001
+    assert lib.musc_msm_rank_f32(8, 10, 0, 2, fake, off, big, None) == 1001
+    assert lib.musc_msm_nearest_f32(fake, 8, 10, 16, fake, off, big, None) == 1001
+    assert lib.musc_msm_split_scores_f32(fake, 8, 300, 16, 0, 2, 0, fake, off, big, None) == 1001
+    assert lib.musc_msm_split_prepare_f32(fake, 8, 300, 16, 0, off, big, None) == 1001
+    assert lib.musc_msm_split_pair_minima(8, 300, 16, off, big, None) == 1001
+    # the refinement validates like the other stages
+    assert lib.musc_msm_refine_f32(None, 8, 10, 16, fake, big, None) == 1001
+    assert lib.musc_msm_refine_f32(fake, 8, 10, 16, fake, ctypes.c_size_t(16), None) == 1002
 
 
 def test_lnamd_argument_errors(lib):
