@@ -355,19 +355,6 @@ int musc_calibrate_mfma_f32(float* out, int blocks, int iters, double* flop, hip
  * instruction): the sustained fp16 MFMA rate of the device. */
 int musc_calibrate_mfma_f16(float* out, int blocks, int iters, double* flop, hipStream_t stream);
 
-/* HBM calibration (no counterpart in the reference; measurement aids).
- * musc_calibrate_hbm_stream: mode 0 reads `bytes` of src (nontemporal loads), 1 writes
- * `bytes` of dst, 2 copies src -> dst; one 16-byte vector per thread in a one-shot
- * grid, the most HBM-friendly pattern (the achievable rate of the part).
- * musc_calibrate_lnamd_pattern: the global access pattern of the LNAMD streaming
- * kernel (tokens (layers, n, tokens_per_image, c) fp32 read once, n_radii writes of
- * (n_radii, layers, n, P, c) fp32) with no arithmetic: the rate the pattern allows.
- * mode 0 replays reads and writes, 1 only the writes, 2 only the reads.
- * c a multiple of 64; 16-byte aligned buffers. */
-int musc_calibrate_hbm_stream(int mode, const void* src, void* dst, long long bytes, hipStream_t stream);
-int musc_calibrate_lnamd_pattern(const float* tokens, float* out, int n, int layers, int tokens_per_image,
-                                 int c, int n_radii, int mode, hipStream_t stream);
-
 #ifdef __cplusplus
 }
 #endif

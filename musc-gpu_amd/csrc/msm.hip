@@ -635,7 +635,11 @@ __global__ __launch_bounds__(kRankRows) void msm_rank_select_kernel(const uint32
   }
   sb += (double)(b - lb) * (double)sqrtf(__uint_as_float(tb));
   if (a > 0) sa += (double)(a - la) * (double)sqrtf(__uint_as_float(ta));
-  scores[row] = (double)(float)((sb - sa) / (double)(b - a));
+  // S(a) is infinite only when the a-th smallest key is +inf: every key of the window
+  // is then +inf or NaN, and the window's mean is S(b) itself (+inf, or NaN when a NaN
+  // falls inside), where S(b) - S(a) would give inf - inf = NaN
+  const double win = isinf(sa) ? sb : sb - sa;
+  scores[row] = (double)(float)(win / (double)(b - a));
 }
 
 // Short windows (b <= 32, every BASELINE configuration): ascending register lists of

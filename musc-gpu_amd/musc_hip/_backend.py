@@ -7,8 +7,12 @@ accelerated path is unavailable; `configure_backend(cfg, device_type)` returns
 cfg itself or a deep-copied super_fast preset.
 
 The accelerated path here is libmusc_hip on a ROCm GPU, so the reference's
-Windows/NVRTC gate (:12-13) becomes "torch is a ROCm build, libmusc_hip.so loads
-and the current device has the architecture its kernels are compiled for".
+Windows/NVRTC gate (:12-13) becomes "torch is a ROCm build, libmusc_hip.so loads,
+a device is visible and it has the architecture the kernels are compiled for".
+Like the reference's selector (:1, "no model loading or CUDA calls"), this one
+starts no GPU runtime: the architecture is compared here only when torch has
+already initialised HIP; otherwise the first launch on each device compares it
+(musc_hip._runtime.stream) and raises RuntimeError on a mismatch.
 `platform` is accepted for signature compatibility and ignored.
 """
 from __future__ import annotations
@@ -29,7 +33,12 @@ def select_backend(requested, device_type, platform=None):
     if torch.version.hip is None:
         return 'original', 'the accelerated runtime requires a ROCm build of PyTorch'
     from . import _runtime
-    ok, reason = _runtime.device_supported()
+    ok, reason = _runtime.available()
+    if ok:
+        if torch.cuda.is_initialized():
+            ok, reason = _runtime.device_supported()
+        elif torch.cuda.device_count() == 0:      # counts devices without starting HIP
+            ok, reason = False, 'no ROCm device is visible'
     if not ok:
         return 'original', reason
     return requested, None

@@ -73,8 +73,6 @@ SIGNATURES = {
     'musc_attention_weights_strided': (_i, [_vp, _vp, _i, _i, _i, _i, _i, _ll, _ll, _ll, _f, _vp, _vp, _sz, _vp]),
     'musc_layernorm_rows': (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _vp]),
     'musc_activation': (_i, [_vp, _vp, _i, _i, _ll, _vp]),
-    'musc_calibrate_hbm_stream': (_i, [_i, _vp, _vp, _ll, _vp]),
-    'musc_calibrate_lnamd_pattern': (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     'musc_calibrate_mfma_f32': (_i, [_vp, _i, _i, ctypes.POINTER(ctypes.c_double), _vp]),
     'musc_calibrate_mfma_f16': (_i, [_vp, _i, _i, ctypes.POINTER(ctypes.c_double), _vp]),
 }
@@ -160,8 +158,23 @@ def check(rc: int, op: str) -> None:
     raise RuntimeError(msg)
 
 
+_supported_devices: set[int] = set()
+
+
 def stream(device: torch.device | int | None = None) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """torch's current stream on `device`, as the handle the C-ABI takes.  The first call
+    for a device checks its architecture against the library's (device_supported) and
+    raises RuntimeError on a mismatch: every launch of this package passes through here,
+    so a device the selector did not examine (it makes no GPU calls before the HIP
+    runtime is up) fails loudly at its first launch instead of faulting."""
+    s = torch.cuda.current_stream(device)
+    index = s.device_index
+    if index not in _supported_devices:
+        ok, reason = device_supported(index)
+        if not ok:
+            raise RuntimeError(reason)
+        _supported_devices.add(index)
+    return s.cuda_stream
 
 
 def require_device_tensor(t: torch.Tensor, name: str) -> None:

@@ -2,9 +2,11 @@
 
     python musc-gpu_amd/musc_hip/build.py [-v]
 
-Every .hip file is compiled to its own object (in parallel), then linked into
-musc-gpu_amd/musc_hip/libmusc_hip.so.  The library is built in-tree so that it
-travels with the source tree to the GPU host.
+Every .hip file under csrc/ is compiled to its own object (in parallel), then
+linked into musc-gpu_amd/musc_hip/libmusc_hip.so, the product library.  The HBM
+measurement probes under measure/ are linked into their own library,
+musc-gpu_amd/measure/libmusc_measure.so, which only kernels_bench.py loads.  Both
+are built in-tree so that they travel with the source tree to the GPU host.
 """
 from __future__ import annotations
 
@@ -17,8 +19,10 @@ import sys
 PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(ROOT, 'csrc')
+MEASURE = os.path.join(ROOT, 'measure')
 BUILD = os.path.join(ROOT, '_build')
 LIB = os.path.join(PKG, 'libmusc_hip.so')
+MEASURE_LIB = os.path.join(MEASURE, 'libmusc_measure.so')
 ARCH = os.environ.get('MUSC_OFFLOAD_ARCH', 'gfx950')
 HIPCC = os.environ.get('HIPCC', '/opt/rocm/bin/hipcc')
 
@@ -51,19 +55,27 @@ def _compile(src: str, verbose: bool) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(BUILD, exist_ok=True)
-    sources = sorted(glob.glob(os.path.join(CSRC, '*.hip')))
-    if not sources:
-        raise RuntimeError(f'no HIP sources under {CSRC}')
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), sources))
-    tmp = LIB + '.tmp'
+def _link(objs: list[str], lib: str, verbose: bool) -> None:
+    tmp = lib + '.tmp'
     cmd = [HIPCC, '-shared', '-fPIC', f'--offload-arch={ARCH}', '-o', tmp] + objs
     if verbose:
         print(' '.join(cmd), flush=True)
     subprocess.run(cmd, check=True)
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = False) -> str:
+    """Build libmusc_hip.so and libmusc_measure.so; returns the product library's path."""
+    os.makedirs(BUILD, exist_ok=True)
+    sources = sorted(glob.glob(os.path.join(CSRC, '*.hip')))
+    probes = sorted(glob.glob(os.path.join(MEASURE, '*.hip')))
+    if not sources:
+        raise RuntimeError(f'no HIP sources under {CSRC}')
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(sources) + len(probes))) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose), sources + probes))
+    _link(objs[:len(sources)], LIB, verbose)
+    if probes:
+        _link(objs[len(sources):], MEASURE_LIB, verbose)
     return LIB
 
 

@@ -154,12 +154,24 @@ def bench_super_fast(args):
             'pair_tflops': flop / (pair / 1e3) / 1e12}
 
 
+def _measure_library():
+    """The HBM measurement probes (musc-gpu_amd/measure/libmusc_measure.so, musc_measure.h),
+    built beside the product library but not part of it."""
+    import ctypes
+    from musc_hip import build
+    lib = ctypes.CDLL(build.MEASURE_LIB)
+    vp, i, ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong
+    lib.musc_measure_hbm_stream.argtypes = [i, vp, vp, ll, vp]
+    lib.musc_measure_lnamd_pattern.argtypes = [vp, vp, i, i, i, i, i, i, vp]
+    lib.musc_measure_hbm_stream.restype = lib.musc_measure_lnamd_pattern.restype = i
+    return lib
+
+
 def bench_hbm(args):
     """Achievable HBM rates (one-shot read / write / copy of 2 GiB) and the rate of the LNAMD
     stream kernel's access pattern replayed without arithmetic at config 2's shape."""
-    import ctypes
     dev = torch.device('cuda:0')
-    lib, s = rt.library(), rt.stream(dev)
+    lib, s = _measure_library(), rt.stream(dev)
     res = {'kernel': 'hbm'}
     nbytes = 2 << 30
     src = torch.zeros(nbytes // 4, dtype=torch.float32, device=dev)
@@ -169,8 +181,8 @@ def bench_hbm(args):
         for it in range(args.iters + 1):
             e0, e1 = _events()
             e0.record()
-            rt.check(lib.musc_calibrate_hbm_stream(mode, src.data_ptr(), dst.data_ptr(), nbytes, s),
-                     'musc_calibrate_hbm_stream')
+            rt.check(lib.musc_measure_hbm_stream(mode, src.data_ptr(), dst.data_ptr(), nbytes, s),
+                     'musc_measure_hbm_stream')
             e1.record()
             torch.cuda.synchronize()
             if it > 0:
@@ -191,8 +203,8 @@ def bench_hbm(args):
         for it in range(args.iters + 1):
             e0, e1 = _events()
             e0.record()
-            rt.check(lib.musc_calibrate_lnamd_pattern(toks.data_ptr(), out.data_ptr(), n, L, T, C, R, mode, s),
-                     'musc_calibrate_lnamd_pattern')
+            rt.check(lib.musc_measure_lnamd_pattern(toks.data_ptr(), out.data_ptr(), n, L, T, C, R, mode, s),
+                     'musc_measure_lnamd_pattern')
             e1.record()
             torch.cuda.synchronize()
             if it > 0:

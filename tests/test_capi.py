@@ -35,6 +35,20 @@ def test_every_declared_symbol_is_exported(lib):
     assert set(names) == set(_runtime.SIGNATURES), 'ctypes signatures out of sync with the header'
 
 
+def test_measurement_probes_live_in_their_own_library(lib):
+    # the HBM probes are working tools: libmusc_measure.so exports what musc_measure.h
+    # declares, and the product library exports none of it
+    from musc_hip import build
+    text = re.sub(r'/\*.*?\*/', '', open(os.path.join(ROOT, 'musc-gpu_amd', 'measure', 'musc_measure.h')).read(),
+                  flags=re.S)
+    names = sorted(set(re.findall(r'\b(musc_\w+)\s*\(', text)))
+    assert names == ['musc_measure_hbm_stream', 'musc_measure_lnamd_pattern']
+    probes = ctypes.CDLL(build.MEASURE_LIB)
+    for name in names:
+        assert hasattr(probes, name) and not hasattr(lib, name)
+    assert not hasattr(lib, 'musc_calibrate_hbm_stream') and not hasattr(lib, 'musc_calibrate_lnamd_pattern')
+
+
 def test_version_and_strerror(lib):
     assert lib.musc_version() >= 100
     assert b'invalid argument' in lib.musc_strerror(1001)

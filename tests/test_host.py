@@ -27,6 +27,7 @@ def _fake_device(monkeypatch, arch):
     """A visible ROCm device of architecture `arch` (gcnArchName as HIP reports it)."""
     monkeypatch.setattr(torch.version, 'hip', torch.version.hip or '7.0')
     monkeypatch.setattr(torch.cuda, 'is_available', lambda: True)
+    monkeypatch.setattr(torch.cuda, 'is_initialized', lambda: True)
     monkeypatch.setattr(torch.cuda, 'current_device', lambda: 0)
     monkeypatch.setattr(torch.cuda, 'get_device_properties', lambda i: SimpleNamespace(gcnArchName=arch))
 
@@ -56,8 +57,43 @@ def test_select_backend_wrong_architecture_falls_back(monkeypatch):
 def test_select_backend_no_visible_device(monkeypatch):
     monkeypatch.setattr(torch.version, 'hip', torch.version.hip or '7.0')
     monkeypatch.setattr(torch.cuda, 'is_available', lambda: False)
-    sel, reason = select_backend('gpu', 'cuda')
-    assert sel == 'original' and 'no ROCm device' in reason
+    monkeypatch.setattr(torch.cuda, 'device_count', lambda: 0)
+    for initialised in (False, True):
+        monkeypatch.setattr(torch.cuda, 'is_initialized', lambda: initialised)
+        sel, reason = select_backend('gpu', 'cuda')
+        assert sel == 'original' and 'no ROCm device' in reason
+
+
+def _no_gpu_calls(monkeypatch):
+    def fail(*a, **k):
+        raise AssertionError('the selector must not start the GPU runtime')
+    for name in ('is_available', 'current_device', 'get_device_properties', 'current_stream', 'init'):
+        monkeypatch.setattr(torch.cuda, name, fail)
+
+
+def test_select_backend_makes_no_gpu_calls_before_hip_starts(monkeypatch):
+    # models/modules/_backend.py:1: "no model loading or CUDA calls"; with the runtime not
+    # yet initialised only the device count is read (it starts no HIP context)
+    monkeypatch.setattr(torch.version, 'hip', torch.version.hip or '7.0')
+    monkeypatch.setattr(torch.cuda, 'is_initialized', lambda: False)
+    monkeypatch.setattr(torch.cuda, 'device_count', lambda: 1)
+    _no_gpu_calls(monkeypatch)
+    assert select_backend('gpu', 'cuda') == ('gpu', None)
+    cfg = deepcopy(CFG)
+    assert configure_backend(cfg, 'cuda')['models']['r_list'] == [3]
+
+
+def test_first_launch_checks_the_architecture(monkeypatch):
+    # the architecture the selector skipped is compared at the first launch on a device
+    from musc_hip import _runtime
+    _fake_device(monkeypatch, 'gfx942:sramecc+:xnack-')
+    monkeypatch.setattr(torch.cuda, 'current_stream',
+                        lambda d=None: SimpleNamespace(device_index=0, cuda_stream=0))
+    monkeypatch.setattr(_runtime, '_supported_devices', set())
+    with pytest.raises(RuntimeError, match='gfx942'):
+        _runtime.stream(0)
+    _fake_device(monkeypatch, 'gfx950:sramecc+:xnack-')
+    assert _runtime.stream(0) == 0 and _runtime._supported_devices == {0}
 
 
 def test_configure_backend_preset_isolated(gfx950):
