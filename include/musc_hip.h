@@ -88,14 +88,15 @@ int musc_msm_scores_f32(const float* z, int n, int p, int c,
  * counterpart in the reference.  For callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  The workspace is a device array inside the library, one per GPU,
- * of MUSC_NOALLOC_SCRATCH_BYTES (64 MiB; held by every GPU the library runs on
+ * of MUSC_NOALLOC_SCRATCH_BYTES (256 MiB, the reference's own scratch cap
+ * (models/modules/_MSM_gpu.py:11); held by every GPU the library runs on
  * until the process ends), so pools whose musc_msm_workspace_bytes exceeds it are
- * rejected with MUSC_ERR_SCRATCH_LIMIT (N = 83, P = 1369 needs 38.6 MB; N = 160,
- * P = 1369 does not fit).  Runs on the current device; `stream` must belong to it.
+ * rejected with MUSC_ERR_SCRATCH_LIMIT (at P = 1369: N = 83 needs 37 MiB, N = 160
+ * 136 MiB; N = 225 does not fit).  Runs on the current device; `stream` must belong to it.
  * Every call on one GPU uses that GPU's array: calls that overlap on one GPU (other
  * streams or threads) race and must be serialised by the caller.  Same arguments
  * (minus the workspace), results and errors as musc_msm_scores_f32. */
-#define MUSC_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+#define MUSC_NOALLOC_SCRATCH_BYTES ((size_t)256 << 20)
 int musc_msm_scores_f32_noalloc(const float* z, int n, int p, int c, int rank_lo, int rank_hi,
                                 double* scores, hipStream_t stream);
 

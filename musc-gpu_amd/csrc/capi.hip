@@ -8,7 +8,7 @@ extern "C" const char* musc_strerror(int code) {
     case MUSC_ERR_WORKSPACE: return "musc: workspace is missing or smaller than required";
     case MUSC_ERR_UNSUPPORTED: return "musc: shape outside the implemented range";
     case MUSC_ERR_SCRATCH_LIMIT:
-      return "musc: the problem's workspace exceeds the no-allocation scratch (MUSC_NOALLOC_SCRATCH_BYTES = 64 MiB); "
+      return "musc: the problem's workspace exceeds the no-allocation scratch (MUSC_NOALLOC_SCRATCH_BYTES = 256 MiB); "
              "use the entry point that takes a workspace";
     default: break;
   }

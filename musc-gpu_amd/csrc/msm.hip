@@ -1040,7 +1040,7 @@ extern "C" int musc_msm_scores_f32(const float* z, int n, int p, int c, int rank
 // ---------------------------------------------------------------------------
 namespace {
 
-constexpr size_t kScratchBytes = size_t(64) << 20;  // MUSC_NOALLOC_SCRATCH_BYTES
+constexpr size_t kScratchBytes = size_t(256) << 20;  // MUSC_NOALLOC_SCRATCH_BYTES
 static_assert(kScratchBytes == MUSC_NOALLOC_SCRATCH_BYTES, "header and library disagree on the scratch size");
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 

@@ -38,9 +38,9 @@ def _no_alloc(z, a, b):
 
 
 def test_no_alloc_matches_the_workspace_entry_point(device):
-    # call 1: the default pool's shape (N = 83, P = 1369, C = 1024: 38.6 MB of workspace);
+    # call 1: config 5's pool shape (N = 160, P = 1369, C = 1024: 136 MiB of workspace);
     # call 2: a smaller pool (stale keys of call 1 lie beyond its minima)
-    for (n, p, c), seed in (((83, 1369, 1024), 42), ((20, 300, 256), 7)):
+    for (n, p, c), seed in (((160, 1369, 1024), 42), ((20, 300, 256), 7)):
         z = synthetic.msm_features(n, p, c, seed=seed).to(device)
         a, b = _MSM_hip.rank_window(n)
         got = _no_alloc(z, a, b)
@@ -53,12 +53,12 @@ def test_no_alloc_matches_the_workspace_entry_point(device):
 
 def test_no_alloc_rejects_pools_beyond_the_scratch(device):
     assert rt.library().musc_target_arch() == b'gfx950'
-    limit = 64 << 20
-    n, p, c = 300, 300, 4            # n * p * n * 4 bytes of minima keys = 108 MB > 64 MiB
+    limit = 256 << 20
+    n, p, c = 600, 200, 4            # n * p * n * 4 bytes of minima keys = 288 MB > 256 MiB
     assert _MSM_hip.workspace_bytes(n, p, c) > limit
     z = torch.zeros((n, p, c), device=device)
     out = torch.zeros((n, p), dtype=torch.float64, device=device)
-    rc = rt.library().musc_msm_scores_f32_noalloc(z.data_ptr(), n, p, c, 0, 89, out.data_ptr(), rt.stream(device))
+    rc = rt.library().musc_msm_scores_f32_noalloc(z.data_ptr(), n, p, c, 0, 179, out.data_ptr(), rt.stream(device))
     assert rc == rt.MUSC_ERR_SCRATCH_LIMIT
     assert b'no-allocation scratch' in rt.library().musc_strerror(rc)
     assert (out == 0).all()          # nothing was launched
