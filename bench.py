@@ -1,7 +1,7 @@
 """Benchmark: MuSc mutual scoring of the default pool on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config pool|plumbing]
-                    [--no-cpu-baseline] [--no-split]
+                    [--no-cpu-baseline] [--no-split] [--no-attention] [--cpu-full]
 
 One step is one pass of the hot path over the whole synthetic pool, inputs
 resident in HBM: LNAMD for every (layer, radius) (window sums of x - mean), the
@@ -18,7 +18,10 @@ average duration from torch.cuda (HIP) events recorded around every launch in
 the timed region on the stream it runs on.  The CPU baseline is the oracle's
 restatement of the reference's original torch backend, timed on a bounded
 sample on this host and extrapolated to the whole job; `config1_full` times
-config 1 in full on both sides, with nothing extrapolated.  The roofline object
+config 1 in full on both sides, with nothing extrapolated.  `--cpu-full` (off by
+default: about six minutes of CPU work) also times the restatement over the whole
+config-2 job once, nothing extrapolated, and gates every score row, map and image
+score against the GPU's (`cpu_baseline_full`).  The roofline object
 also carries this box's sustained fp32 MFMA rate (a calibration kernel with no
 memory traffic, run after the timed steps): the part's clock differs from box
 to box, and the datasheet peak assumes the highest.
@@ -64,19 +67,45 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def profiled_traffic(config: str):
+TRAFFIC_PROFILE = os.path.join('profiles', 'msm_lnamd_hbm_traffic_config2.md')
+PAIR_KERNEL_SOURCES = (os.path.join('musc-gpu_amd', 'csrc', 'msm.hip'),
+                       os.path.join('musc-gpu_amd', 'csrc', 'msm_common.hpp'))
+
+
+def pair_kernel_source_digest() -> str:
+    """sha256 over the sources the fp32 pair kernel is compiled from."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in PAIR_KERNEL_SOURCES:
+        with open(os.path.join(ROOT, rel), 'rb') as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+def profiled_traffic(config: str) -> dict:
     """HBM bytes per msm_pair_min_kernel launch from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary (copy-kernel calibrated), or None when no summary covers `config`."""
+    WRITE_SIZE summary (copy-kernel calibrated).  The summary records the digest of the
+    sources it was measured on; when the current sources differ the figure belongs to
+    another kernel, so `bytes` is None and `stale` says why."""
+    out = {'bytes': None, 'source': TRAFFIC_PROFILE + ' (rocprofv3 PMC FETCH_SIZE + WRITE_SIZE, copy-calibrated)'}
     if config != 'pool':
-        return None
-    path = os.path.join(ROOT, 'profiles', 'msm_lnamd_hbm_traffic_config2.md')
+        out['stale'] = 'no summary covers this configuration'
+        return out
+    value, digest = None, None
     try:
-        for line in open(path):
+        for line in open(os.path.join(ROOT, TRAFFIC_PROFILE)):
             if line.startswith('traffic_bytes_per_launch msm_pair_min_kernel config2:'):
-                return float(line.split(':')[1])
+                value = float(line.split(':')[1])
+            elif line.startswith('pair_kernel_source_sha256:'):
+                digest = line.split(':')[1].strip()
     except OSError:
-        pass
-    return None
+        out['stale'] = 'summary missing'
+        return out
+    if digest != pair_kernel_source_digest():
+        out['stale'] = 'the summary was measured on other pair-kernel sources; re-profile to report traffic'
+        return out
+    out['bytes'] = value
+    return out
 
 
 def host_cpus() -> dict:
@@ -215,6 +244,54 @@ def cpu_baseline(tokens_cpu, pools_gpu, scores_gpu, maps_gpu, r_list, image_size
         'extrapolated_seconds': total,
         'agreement': gate,
     }
+
+
+def cpu_baseline_full(tokens_cpu, scores_gpu, maps_gpu, img_gpu, r_list, image_size):
+    """The oracle's torch CPU restatement of the original backend over the whole job, once
+    (nothing extrapolated): LNAMD Unfold path for every image in the reference's batches of
+    4 (_LNAMD.py:72-129), L2 normalisation, compute_scores_fast for every query image of
+    every (radius, layer) pool (_MSM.py:10-30,53-59), the epilogue (musc.py:259-288).  Every
+    score row, map and image score is compared with the GPU's (compare_arrays)."""
+    import torch
+    from musc_hip import agreement
+    from oracle import epilogue as oe
+    from oracle import lnamd as ol
+    from oracle import msm as om
+
+    cpus = host_cpus()
+    torch.set_num_threads(cpus['usable_cpus'])
+    n, n_layers, n_r = tokens_cpu[0].shape[0], len(tokens_cpu), len(r_list)
+    ref = torch.empty(scores_gpu.shape, dtype=torch.float64)
+    t_lnamd = t_msm = 0.0
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        for ri, r in enumerate(r_list):
+            t1 = time.perf_counter()
+            feats = torch.cat([ol.lnamd_embed([t[s:s + 4] for t in tokens_cpu], r) for s in range(0, n, 4)], 0)
+            feats = ol.l2_normalise(feats)
+            t2 = time.perf_counter()
+            t_lnamd += t2 - t1
+            for li in range(n_layers):
+                ref[ri, li] = om.MSM(feats[:, :, li, :].contiguous())
+                log(f'[bench] cpu full: radius {r} layer {li} scored ({time.perf_counter() - t0:.0f} s so far)')
+            t_msm += time.perf_counter() - t2
+            del feats
+        t3 = time.perf_counter()
+        ref_maps, ref_img = oe.maps_and_scores([[ref[ri, li] for li in range(n_layers)] for ri in range(n_r)],
+                                               image_size)
+        t_epi = time.perf_counter() - t3
+    total = time.perf_counter() - t0
+    gate = {'msm_score_rows': agreement.compare_arrays(ref.reshape(-1, ref.shape[-1]),
+                                                        scores_gpu.cpu().reshape(-1, ref.shape[-1])),
+            'maps': agreement.compare_arrays(ref_maps, maps_gpu.cpu()),
+            'image_scores': agreement.compare_arrays(ref_img, img_gpu.cpu())}
+    gate['pass'] = all(g['pass'] for g in gate.values())
+    return {'value': n / total, 'unit': 'images/s', 'cores': cpus['usable_cpus'], 'kind': 'port',
+            'torch_threads': torch.get_num_threads(), 'host': cpus, 'extrapolated': False, 'runs': 1,
+            'seconds': total, 'lnamd_s': t_lnamd, 'msm_s': t_msm, 'epilogue_s': t_epi,
+            'sample': f'the whole job: LNAMD on all {n} images x {n_layers} layers x radii {r_list}, '
+                      f'compute_scores_fast for all {n} query images of all {n_r * n_layers} pools, the epilogue',
+            'agreement': gate}
 
 
 def sustained_fp32_mfma_tflops(dev, reps: int = 3) -> float:
@@ -359,6 +436,8 @@ def main() -> int:
     ap.add_argument('--no-split', action='store_true',
                     help='skip the second measurement with the split (3x fp16 MFMA) MSM engine')
     ap.add_argument('--no-attention', action='store_true', help='skip the config-4 attention measurement')
+    ap.add_argument('--cpu-full', action='store_true',
+                    help='also time the CPU restatement over the whole config-2 job (about six minutes)')
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU only: this build has no multi-GPU path (--gpus {args.gpus} requested). '
@@ -426,6 +505,8 @@ def main() -> int:
 
     pair_ms = [a.elapsed_time(b) for a, b in timing['pairs']]
     rank_ms = [a.elapsed_time(b) for a, b in timing['rank']]
+    refine_ms = [a.elapsed_time(b) for a, b in timing['refine']]
+    refine_avg_s = sum(refine_ms) / len(refine_ms) / 1e3
     rank_avg_s = sum(rank_ms) / len(rank_ms) / 1e3
     rank_bytes = 4.0 * n * p * n + 8.0 * n * p        # minima keys read once, float64 scores written
     rank_gbps = rank_bytes / rank_avg_s / 1e9
@@ -437,6 +518,7 @@ def main() -> int:
     lnamd_avg_s = sum(lnamd_ms) / len(lnamd_ms) / 1e3
     lnamd_gbps = lnamd_bytes / lnamd_avg_s / 1e9
 
+    traffic = profiled_traffic(args.config)
     result = {
         'metric': 'MSM pool images/sec + fp32 MFMA TFLOP/s (% peak), 83-image 37x37x1024 pool',
         'value': n * args.steps / elapsed,
@@ -457,8 +539,9 @@ def main() -> int:
                    'seed': args.seed},
         'roofline': {'bound': 'mfma', 'kernel': 'msm_pair_min_kernel',
                      'achieved': achieved_tflops, 'peak': FP32_MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
-                     'frac': achieved_tflops / FP32_MFMA_PEAK_TFLOPS, 'traffic': profiled_traffic(args.config),
-                     'traffic_source': 'profiles/msm_lnamd_hbm_traffic_config2.md (rocprofv3 PMC, copy-calibrated)',
+                     'frac': achieved_tflops / FP32_MFMA_PEAK_TFLOPS, 'traffic': traffic['bytes'],
+                     'traffic_source': traffic['source'],
+                     **({'traffic_stale': traffic['stale']} if 'stale' in traffic else {}),
                      'flop_per_launch': flop_per_launch, 'avg_launch_ms': pair_avg_s * 1e3,
                      'launches': len(pair_ms),
                      'box_sustained_tflops': box_sustained,
@@ -473,7 +556,12 @@ def main() -> int:
                                                         else 'msm_rank_select_kernel'), 'achieved': rank_gbps,
                              'peak': HBM_PEAK_GBPS, 'unit': 'GB/s', 'frac': rank_gbps / HBM_PEAK_GBPS,
                              'algorithmic_bytes': rank_bytes, 'avg_launch_ms': rank_avg_s * 1e3,
-                             'launches': len(rank_ms)}},
+                             'launches': len(rank_ms)},
+                    'refine': {'bound': 'hbm', 'kernel': 'msm_refine_kernel', 'avg_launch_ms': refine_avg_s * 1e3,
+                               'launches': len(refine_ms),
+                               'achieved': 4.0 * n * p * n / refine_avg_s / 1e9, 'unit': 'GB/s',
+                               'note': 'cancellation refinement: one read of the minima keys when nothing is '
+                                       'flagged (none is in this pool)'}},
         'agreement': {'evaluated': False},
         'cpu_baseline': None,
     }
@@ -543,6 +631,13 @@ def main() -> int:
             result['value'] = None
             result['value_withheld_reason'] = 'GPU results fail the 2e-5 agreement gate against the oracle sample'
         log('[bench] CPU baseline done')
+        if args.config == 'pool' and args.cpu_full:
+            try:
+                result['cpu_baseline_full'] = cpu_baseline_full(tokens_cpu, scores, maps, img, r_list, image_size)
+                log('[bench] CPU restatement timed over the whole job')
+            except Exception as exc:  # noqa: BLE001
+                result['cpu_baseline_full'] = {'error': repr(exc)}
+                log(f'[bench] full CPU timing failed: {exc!r}')
         if args.config == 'pool':
             del pools, scores
             try:

@@ -44,14 +44,15 @@ def lnamd_pools(tokens: list[torch.Tensor], r_list: list[int], pool_grid: int | 
 
 def msm_all(pools: torch.Tensor, topmin_min: float = 0, topmin_max: float = 0.3,
             pair_events: list | None = None, normalize_rows: bool = True, engine: str = 'fp32',
-            rank_events: list | None = None) -> torch.Tensor:
+            rank_events: list | None = None, refine_events: list | None = None) -> torch.Tensor:
     """(R, L, N, P) float64 MSM maps of every (radius, layer) pool.
 
     Runs the three MSM stages explicitly (prepare, pair minima, rank) so that a
     caller can pass `pair_events`, a list that receives one (start, end)
     torch.cuda.Event pair recorded around each pair-minima kernel on the stream
-    it runs on (`rank_events` the same around each rank kernel).  `engine` selects
-    how the dot products are formed ('fp32' or 'split16', see _MSM_hip).
+    it runs on (`rank_events` and `refine_events` the same around each rank and
+    cancellation-refinement kernel).  `engine` selects how the dot products are
+    formed ('fp32' or 'split16', see _MSM_hip).
     """
     rt.require_device_tensor(pools, 'pools')
     if pools.ndim != 5 or pools.dtype != torch.float32 or not pools.is_contiguous():
@@ -89,8 +90,14 @@ def msm_all(pools: torch.Tensor, topmin_min: float = 0, topmin_max: float = 0.3,
                 if pair_events is not None:
                     ev[1].record()
                     pair_events.append(ev)
+                if refine_events is not None:
+                    fev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                    fev[0].record()
                 rt.check(lib.musc_msm_refine_f32(z.data_ptr(), n, p, c, ws.data_ptr(), ws.numel(), s),
                          'musc_msm_refine_f32')
+                if refine_events is not None:
+                    fev[1].record()
+                    refine_events.append(fev)
                 if rank_events is not None:
                     rev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                     rev[0].record()
@@ -108,8 +115,9 @@ def score_pool(tokens: list[torch.Tensor], r_list=(1, 3, 5), image_size: int = 5
     """Tokens (list over layers of (N, 1+P, C) GPU tensors) -> (maps (N,1,S,S) f64, image scores (N,) f64).
 
     `timing`, if given, receives torch.cuda.Event pairs: timing['lnamd'] (one
-    pair around the LNAMD launch), timing['pairs'] (one per MSM pair kernel) and
-    timing['rank'] (one per MSM rank kernel).
+    pair around the LNAMD launch), timing['pairs'] (one per MSM pair kernel),
+    timing['refine'] (one per refinement kernel) and timing['rank'] (one per MSM
+    rank kernel).
     `pool_grid` (the super_fast profile: 28) adaptively pools every patch grid to
     pool_grid x pool_grid before scoring (models/modules/_super_fast.py:17-27).
     `msm_engine` selects the MSM dot-product engine ('fp32' or 'split16').
@@ -124,7 +132,8 @@ def score_pool(tokens: list[torch.Tensor], r_list=(1, 3, 5), image_size: int = 5
         timing.setdefault('lnamd', []).append(lnamd_ev)
     scores = msm_all(pools, topmin_min, topmin_max,
                      pair_events=timing.setdefault('pairs', []) if timing is not None else None, engine=msm_engine,
-                     rank_events=timing.setdefault('rank', []) if timing is not None else None)
+                     rank_events=timing.setdefault('rank', []) if timing is not None else None,
+                     refine_events=timing.setdefault('refine', []) if timing is not None else None)
     del pools
     return _epilogue_hip.maps_and_scores(scores, image_size, want_maps=want_maps)
 

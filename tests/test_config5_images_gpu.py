@@ -28,14 +28,19 @@ torch's bmm for both products, its own softmax with fp32 max and sum over the fp
 logits and P = fp16(exp(l - max) / sum)) is that kind of change.  The test restates it
 in torch ops (F.softmax replaced while the math path runs, as the reference does),
 measures its distance from the math path beside the product's, and gates the product
-at twice that distance or 2e-5, whichever is larger.
+at twice that distance or 2e-5, whichever is larger.  It also runs the product path
+with its fused attention replaced by the same restatement (the math path's rounding
+points: fp16 logits, fp32 max and sum, P = fp16(exp(l - max) / sum), fp16 P.V): the
+maps then move by as much as the product's own do, so aligning the attention's
+rounding points does not bring the fp16 comparison under 2e-5 either -- the
+LayerNorm and patch-embedding reduction orders alone move them that far.
 """
 import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F
 
-from musc_hip import pipeline, synthetic, vit
+from musc_hip import _attention_hip, pipeline, synthetic, vit
 from oracle import epilogue as oe
 from oracle import lnamd as ol
 from oracle import msm as om
@@ -72,6 +77,18 @@ def _reference_design_softmax(input, dim=None, _stacklevel=3, dtype=None):
         e = torch.exp(x - x.amax(-1, keepdim=True))
         return e / e.sum(-1, keepdim=True)
     return _F_SOFTMAX(input, dim=dim, _stacklevel=_stacklevel, dtype=dtype)
+
+
+def _reference_design_attention_packed(qkv, heads, scale):
+    """The fused attention's place in the product path taken by the reference design's
+    arithmetic in torch ops: softmax(q k^T * scale) v from the packed (T, B, 3E)
+    in-projection, with torch's bmm for both products and _reference_design_softmax."""
+    t, b, e3 = qkv.shape
+    e = e3 // 3
+    q, k, v = (qkv[..., i * e:(i + 1) * e].reshape(t, b * heads, 64).transpose(0, 1) for i in range(3))
+    p = _reference_design_softmax(torch.bmm(q * scale, k.transpose(1, 2).contiguous()), dim=-1)
+    o = torch.bmm(p.to(v.dtype), v.contiguous())
+    return o.transpose(0, 1).reshape(t, b, e)
 
 
 def _encode_math(model, imgs, autocast, softmax=None):
@@ -163,7 +180,7 @@ def test_config5_fp32_from_images_both_engines(setup):
     assert ok, info
 
 
-def test_config5_fp16_from_images_within_reference_design_spread(setup):
+def test_config5_fp16_from_images_within_reference_design_spread(setup, monkeypatch):
     model, imgs = setup
     ref_tok, _ = _encode_math(model, imgs, autocast=True)
     ref_maps, ref_img = _oracle_chain(ref_tok)
@@ -185,3 +202,12 @@ def test_config5_fp16_from_images_within_reference_design_spread(setup):
         print(f'config5 fp16 from images ({what}): maps {em:.3e}, image scores {ei:.3e} '
               f'(gate {gate[0]:.2e} / {gate[1]:.2e})', flush=True)
         assert em <= gate[0] and ei <= gate[1]
+    del out, split_maps, split_img
+    # the product path with the math path's attention rounding points
+    monkeypatch.setattr(_attention_hip, 'attention_packed', _reference_design_attention_packed)
+    aligned = pipeline.run_category(model, imgs, feature_layers=LAYERS, r_list=R_LIST, batch_size=4,
+                                    k_list=K_LIST, autocast=True)
+    em, ei = _max_err(aligned['maps'], ref_maps), _max_err(aligned['image_scores'], ref_img)
+    print(f'config5 fp16 from images, product path with the reference design attention: maps {em:.3e}, '
+          f'image scores {ei:.3e}', flush=True)
+    assert em <= gate[0] and ei <= gate[1]
