@@ -725,39 +725,60 @@ __global__ __launch_bounds__(kWave) void msm_rank_insert2_kernel(const uint32_t*
   scores[row] = (double)(float)(sum / (double)(b - a));
 }
 
-// Rows of more than 192 images: one wave per row, the n keys staged in LDS and each
-// key's rank counted (ties broken by image index).
+// Rows of more than 192 images: one wave per row.  Slot i of lane l holds key 64 i + l of
+// the row (the own image and the slots past n hold kNoKey, which no threshold counts),
+// and the a-th and b-th smallest keys are found by the same 32-step search over the key
+// bits as msm_rank_select_kernel.  Each count #{key < t} is the sum over slots of the
+// popcount of a ballot (one compare per slot, the sum wave-uniform in scalar registers,
+// no cross-lane reduction), so a row costs 64 ceil(n / 64) compares where counting every
+// key's rank cost n^2 / 64 per lane (16 ms against 4 ms per call at N = 400, P = 1369).
 constexpr int kRankWaves = 4;
 constexpr int kMaxSelectKeys = 192;
 
-__global__ __launch_bounds__(kRankWaves * kWave) void msm_rank_kernel(
-    const uint32_t* __restrict__ minbits, int rows, int n, int p, int a, int b,
-    double* __restrict__ scores) {
-  extern __shared__ uint32_t s_keys[];  // kRankWaves * n
+template <int kSlots>
+__global__ __launch_bounds__(kRankWaves * kWave) void msm_rank_wave_kernel(
+    const uint32_t* __restrict__ minbits, int rows, int n, int p, int a, int b, double* __restrict__ scores) {
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const long long row = (long long)blockIdx.x * kRankWaves + wave;
-  uint32_t* keys = s_keys + wave * n;
-  const bool active = row < rows;
-  const int self = active ? (int)(row / p) : -1;
-  if (active) {
-    for (int j = lane; j < n; j += kWave) keys[j] = j == self ? kNoKey : key_bits(minbits[row * n + j]);
+  if (row >= rows) return;
+  const int self = (int)(row / p);
+  const uint32_t* src = minbits + row * n;
+  uint32_t key[kSlots];
+#pragma unroll
+  for (int i = 0; i < kSlots; ++i) {
+    const int j = i * kWave + lane;
+    key[i] = (j < n && j != self) ? key_bits(src[j]) : kNoKey;
   }
-  __syncthreads();
-  if (!active) return;
-  double sum = 0.0;
-  for (int j = lane; j < n; j += kWave) {
-    if (j == self) continue;
-    const uint32_t v = keys[j];
-    int rank = 0;
-    for (int k = 0; k < n; ++k) {
-      if (k == self) continue;
-      const uint32_t u = keys[k];
-      rank += (u < v) || (u == v && k < j);
+  auto below = [&](uint32_t t) {  // #{key < t} over the row, the same in every lane
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) cnt += __popcll(__ballot(key[i] < t));
+    return cnt;
+  };
+  uint32_t ta = 0, tb = 0;  // a-th and b-th smallest keys (ta stays 0 for a = 0)
+#pragma unroll 1
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cb = tb | (1u << bit);
+    if (below(cb) < b) tb = cb;
+    if (a > 0) {
+      const uint32_t ca = ta | (1u << bit);
+      if (below(ca) < a) ta = ca;
     }
-    if (rank >= a && rank < b) sum += (double)sqrtf(__uint_as_float(v));
   }
-  sum = wave_sum(sum);
-  if (lane == 0) scores[row] = (double)(float)(sum / (double)(b - a));
+  double sa = 0.0, sb = 0.0;
+#pragma unroll
+  for (int i = 0; i < kSlots; ++i) {
+    const double r = (double)sqrtf(__uint_as_float(key[i]));
+    if (key[i] < tb) sb += r;
+    if (key[i] < ta) sa += r;
+  }
+  sb = wave_sum(sb);
+  sa = wave_sum(sa);
+  sb += (double)(b - below(tb)) * (double)sqrtf(__uint_as_float(tb));
+  if (a > 0) sa += (double)(a - below(ta)) * (double)sqrtf(__uint_as_float(ta));
+  // as in msm_rank_select_kernel: an infinite S(a) means a window of +inf (or NaN) keys
+  const double win = isinf(sa) ? sb : sb - sa;
+  if (lane == 0) scores[row] = (double)(float)(win / (double)(b - a));
 }
 
 __global__ __launch_bounds__(256) void msm_nearest_kernel(const uint32_t* __restrict__ minbits,
@@ -890,7 +911,7 @@ inline int validate(const float* z, int n, int p, int c, void* ws, size_t ws_byt
   if (!z || n < 2 || p < 1 || c < 1) return MUSC_ERR_INVALID_ARG;
   const long long rows = (long long)n * p;
   if (rows > (1LL << 30)) return MUSC_ERR_UNSUPPORTED;
-  if (n > 4096) return MUSC_ERR_UNSUPPORTED;  // rank kernel stages n floats per wave in LDS (64 KB)
+  if (n > 4096) return MUSC_ERR_UNSUPPORTED;  // rank kernels hold a row's n keys in at most 64 slots per lane
   if (!ws || ws_bytes < workspace_bytes(n, p)) return MUSC_ERR_WORKSPACE;
   if (!ws_aligned(ws)) return MUSC_ERR_INVALID_ARG;
   if ((c & 3) == 0 && (reinterpret_cast<uintptr_t>(z) & 15) != 0) return MUSC_ERR_INVALID_ARG;
@@ -968,9 +989,15 @@ int run_rank(int n, int p, int a, int b, double* scores, const Workspace& w, hip
 #undef MUSC_RANK_LAUNCH
     return check_launch();
   }
-  const size_t smem = (size_t)kRankWaves * n * sizeof(uint32_t);
-  hipLaunchKernelGGL(msm_rank_kernel, dim3((unsigned)((rows + kRankWaves - 1) / kRankWaves)),
-                     dim3(kRankWaves * kWave), smem, s, w.minbits, (int)rows, n, p, a, b, scores);
+  const dim3 grid((unsigned)((rows + kRankWaves - 1) / kRankWaves)), block(kRankWaves * kWave);
+#define MUSC_RANK_WAVE(K) \
+  hipLaunchKernelGGL(msm_rank_wave_kernel<K>, grid, block, 0, s, w.minbits, (int)rows, n, p, a, b, scores)
+  if (n <= 256) MUSC_RANK_WAVE(4);
+  else if (n <= 512) MUSC_RANK_WAVE(8);
+  else if (n <= 1024) MUSC_RANK_WAVE(16);
+  else if (n <= 2048) MUSC_RANK_WAVE(32);
+  else MUSC_RANK_WAVE(64);  // n <= 4096 (validate)
+#undef MUSC_RANK_WAVE
   return check_launch();
 }
 

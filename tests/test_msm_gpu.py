@@ -172,11 +172,13 @@ def test_normalize_rows_equals_normalised_input(device):
     np.testing.assert_allclose(raw, om.MSM(z).numpy(), rtol=0, atol=1e-4)
 
 
-@pytest.mark.parametrize('n', [2, 3, 31, 32, 33, 64, 65, 96, 97, 128, 129, 160, 161, 192, 193, 200])
+@pytest.mark.parametrize('n', [2, 3, 31, 32, 33, 64, 65, 96, 97, 128, 129, 160, 161, 192, 193, 200, 256, 257,
+                               513, 1025])
 def test_rank_selection_across_register_sizes(device, n):
-    # the rank kernel keeps a row's n minima in registers for n <= 192 (instantiations of
-    # 32/64/96/128/160/192 keys) and counts ranks in LDS beyond; every boundary, windows
-    # starting above 0, and ties.  Small-integer features make every norm and dot product
+    # the rank kernels keep a row's n minima in registers: one lane per row for n <= 192
+    # (instantiations of 32/64/96/128/160/192 keys), one wave per row beyond (4/8/16/32 slots
+    # per lane up to 256/512/1024/2048 images); every boundary, windows starting above 0, and
+    # ties.  Small-integer features make every norm and dot product
     # exact in fp32, so both sides see the same squared distances (integers) and ties are
     # exact: many equal minima, and image 1 duplicates image 0 (zero distances).
     g = torch.Generator().manual_seed(n)

@@ -91,16 +91,19 @@ def test_infinite_minima_below_the_window_start(device):
     # rows that are negative in that channel: +inf + inf in the expanded form), with a
     # window starting above 0 and b > 32 (the bit-search rank kernel, n <= 192): the
     # window holds only +inf, so the score is +inf (the reference's mean of topk values)
-    g = torch.Generator().manual_seed(11)
-    z = torch.randn((120, 16, 64), generator=g)
-    z[:, :, 5] = -z[:, :, 5].abs() - 0.1
-    z[3, 8, 5] = float('inf')
-    zd = z.to(device)
-    for lo, hi in ((0.1, 0.3), (0.0, 0.3), (0.2, 0.9)):
-        got = _MSM_hip.MSM(zd, topmin_min=lo, topmin_max=hi).cpu()
-        ref = om.MSM(z, lo, hi)
-        _check(ref.numpy(), got.numpy(), f'+inf minima, window ({lo}, {hi})')
-        assert got[3, 8] == float('inf')
+    # n = 300: the one-wave-per-row kernel (n > 192), same rule
+    for n in (120, 300):
+        g = torch.Generator().manual_seed(11)
+        z = torch.randn((n, 16, 64), generator=g)
+        z[:, :, 5] = -z[:, :, 5].abs() - 0.1
+        z[3, 8, 5] = float('inf')
+        z[7, 2] = float('nan')                    # NaN minima rank last in every other row
+        zd = z.to(device)
+        for lo, hi in ((0.1, 0.3), (0.0, 0.3), (0.2, 0.9)):
+            got = _MSM_hip.MSM(zd, topmin_min=lo, topmin_max=hi).cpu()
+            ref = om.MSM(z, lo, hi)
+            _check(ref.numpy(), got.numpy(), f'n={n}: +inf minima, window ({lo}, {hi})')
+            assert got[3, 8] == float('inf')
 
 
 def test_small_pools_through_the_lds_epilogue(device):
