@@ -68,8 +68,11 @@ def log(msg: str) -> None:
 
 
 TRAFFIC_PROFILE = os.path.join('profiles', 'msm_lnamd_hbm_traffic_config2.md')
-PAIR_KERNEL_SOURCES = (os.path.join('musc-gpu_amd', 'csrc', 'msm.hip'),
-                       os.path.join('musc-gpu_amd', 'csrc', 'msm_common.hpp'))
+# what msm_pair_min_kernel is compiled from (its file, the headers it includes, the build flags)
+PAIR_KERNEL_SOURCES = (os.path.join('musc-gpu_amd', 'csrc', 'msm_pair.hip'),
+                       os.path.join('musc-gpu_amd', 'csrc', 'msm_common.hpp'),
+                       os.path.join('musc-gpu_amd', 'csrc', 'common.hpp'),
+                       os.path.join('musc-gpu_amd', 'musc_hip', 'build.py'))
 
 
 def pair_kernel_source_digest() -> str:

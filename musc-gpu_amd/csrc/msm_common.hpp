@@ -216,6 +216,9 @@ inline void launch_image_max(const float* norms, int n, int p, uint32_t* imgmax,
   hipLaunchKernelGGL(image_max_kernel<0>, dim3((unsigned)n), dim3(256), 0, s, norms, p, imgmax);
 }
 
+// The fp32 MFMA pair-minima kernel (msm_pair.hip): leaves the squared minima keys.
+int run_pairs(const float* z, int n, int p, int c, const Workspace& w, hipStream_t s);
+
 // Trimmed rank means over the minima (defined in msm.hip, shared by both engines).
 int run_rank(int n, int p, int a, int b, double* scores, const Workspace& w, hipStream_t s);
 
