@@ -36,7 +36,10 @@ fp32 engine's maps; `--no-split` skips it.  The headline stays the fp32 engine.
 timed GPU-paced (every launch queued behind a short spin kernel, so the events
 measure the kernels and not the Python wrapper's per-call overhead), with its
 MFMA roofline and the first and last blocks checked against a float64
-softmax(q k^T / 8) v; `--no-attention` skips it.
+softmax(q k^T / 8) v; beside it, on the same fp16 inputs, the same products in
+torch ops (torch.bmm with torch's softmax, the math path, and with the
+reference's fp32-statistics softmax, its accelerated encoder's design), timed
+and checked the same way; `--no-attention` skips it.
 """
 from __future__ import annotations
 
@@ -423,9 +426,56 @@ def attention_config4(seed: int, iters: int = 3) -> dict:
                      'frac': tf / peak, 'max_abs_err_vs_float64': worst,
                      'tolerance': f'{tol} + {tol} * max|ref| (first and last block)', 'pass': ok}
         del blocks
-    del blocks32
+    # the reference's design for the same products, restated in torch ops on the same inputs:
+    # torch's bmm for q k^T and P v with (a) torch's softmax (the math path of
+    # nn.MultiheadAttention under fp16 autocast) and (b) the reference's accelerated softmax
+    # (models/modules/_attention_gpu.py:41-81,141-146: fp32 maximum and sum over the fp16
+    # logits, P = fp16(exp(l - max) / sum)); k^T is made contiguous before the timed region
+    blocks = [(q.half() * scale, k.half().transpose(1, 2).contiguous(), v.half()) for q, k, v in blocks32]
+    for name, softmax in (('torch_math_path_fp16', lambda x: torch.softmax(x, -1)),
+                          ('reference_design_fp16', _fp32_stats_softmax)):
+        worst, ok = 0.0, True
+        for (qs, kt, v), (q, k, _) in ((blocks[0], blocks32[0]), (blocks[-1], blocks32[-1])):
+            o = torch.bmm(softmax(torch.bmm(qs, kt)), v).double()
+            q64, k64, v64 = q.half().double(), k.half().double(), v.double()
+            ref = torch.bmm(torch.softmax(torch.bmm(q64 * scale, k64.transpose(1, 2).contiguous()), -1), v64)
+            err = (o - ref).abs().max().item()
+            worst = max(worst, err)
+            ok = ok and err <= 2e-4 + 2e-4 * ref.abs().max().item()
+            del o, q64, k64, v64, ref
+        ts = []
+        for it in range(iters + 1):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda._sleep(10_000_000)
+            e0.record()
+            for qs, kt, v in blocks:
+                torch.bmm(softmax(torch.bmm(qs, kt)), v)
+            e1.record()
+            torch.cuda.synchronize()
+            if it:
+                ts.append(e0.elapsed_time(e1) / len(blocks))
+        ms = sum(ts) / len(ts)
+        tf = flop / (ms / 1e3) / 1e12
+        out[name] = {'ops': 'torch.bmm (hipBLASLt) + ' + (
+                         'torch.softmax' if name.startswith('torch') else
+                         'fp32-statistics softmax as unfused torch ops (the reference runs it as one kernel, '
+                         'so this overstates that design\'s cost)') + ' + torch.bmm',
+                     'ms_per_block': ms, 'achieved': tf, 'peak': FP16_MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
+                     'frac': tf / FP16_MFMA_PEAK_TFLOPS, 'fused_fp16_speedup': ms / out['fp16']['ms_per_block'],
+                     'max_abs_err_vs_float64': worst, 'tolerance': '0.0002 + 0.0002 * max|ref| (first and last block)',
+                     'pass': ok}
+    del blocks, blocks32
     torch.cuda.empty_cache()
     return out
+
+
+def _fp32_stats_softmax(x):
+    """Softmax over the last axis of fp16 logits with fp32 maximum and sum, P rounded to fp16
+    (models/modules/_attention_gpu.py:41-81)."""
+    import torch
+    y = x.float()
+    e = torch.exp(y - y.amax(-1, keepdim=True))
+    return (e / e.sum(-1, keepdim=True)).to(x.dtype)
 
 
 def main() -> int:
@@ -615,7 +665,9 @@ def main() -> int:
             result['attention_config4'] = attention_config4(args.seed)
             a4 = result['attention_config4']
             log(f"[bench] config-4 attention: fp32 {a4['fp32']['achieved']:.1f} TFLOP/s, "
-                f"fp16 {a4['fp16']['achieved']:.1f} TFLOP/s")
+                f"fp16 {a4['fp16']['achieved']:.1f} TFLOP/s; torch ops: math path "
+                f"{a4['torch_math_path_fp16']['achieved']:.1f}, reference design "
+                f"{a4['reference_design_fp16']['achieved']:.1f} TFLOP/s")
         except Exception as exc:  # noqa: BLE001
             result['attention_config4'] = {'error': repr(exc)}
             log(f'[bench] config-4 attention failed: {exc!r}')
