@@ -21,12 +21,13 @@ constexpr int BN = 128;          // tile columns (reference patches)
 constexpr int BK = 16;           // K chunk (channels) per pipeline stage: the double-buffered
                                  // stage is 40 KB of LDS, so three workgroups share a CU
                                  // (three waves per SIMD cover each other's epilogues and barriers)
-constexpr int PITCH = BK + 4;    // LDS row pitch in floats for staged operands
+constexpr int PITCH = BK;        // LDS row pitch in floats for staged operands (64 bytes)
 constexpr int EPITCH = BN + 1;   // LDS row pitch of the epilogue distance tile
 constexpr int THREADS = 256;     // 4 waves, each owns a 64x64 sub-tile
 constexpr int kRowsPerPass = THREADS / (BK / 4);  // rows one 16-byte load per thread covers
 constexpr int kPasses = BM / kRowsPerPass;         // such loads per thread per staged operand
 
+static_assert(BK == 16 && kRowsPerPass % 16 == 0, "the segment swizzle assumes 4 segments per row");
 constexpr int kStageFloats = 2 * (BM + BN) * PITCH;       // double-buffered A and B
 constexpr int kEpiFloats = BM * EPITCH;
 constexpr int kSmemFloats = kStageFloats > kEpiFloats ? kStageFloats : kEpiFloats;
@@ -69,10 +70,18 @@ __device__ inline void load_chunk(const float* __restrict__ z, int rows, int c, 
   }
 }
 
+// A staged row is four 16-byte segments; segment s of row r sits at s ^ seg_swizzle(r).
+// The LDS serves 16 lanes of a 16-byte access per 256-byte window: in the operand reads
+// they are 16 consecutive rows at one segment, in the stores 4 rows x 4 segments, and
+// with the swizzle both land on 16 distinct bank groups (without it, rows r and r + 4
+// of a 64-byte pitch, or r and r + 3 of an 80-byte one, share banks).
+__device__ inline int seg_swizzle(int row) { return (row >> 2) & 3; }
+
 __device__ inline void store_chunk(float* __restrict__ dst, const stage4 (&reg)[kPasses]) {
   const int t = threadIdx.x;
   const int lrow = t / (BK / 4);
-  const int lk = (t % (BK / 4)) * 4;
+  // kRowsPerPass is a multiple of 16, so every pass of this thread has the same swizzle
+  const int lk = ((t % (BK / 4)) ^ seg_swizzle(lrow)) * 4;
 #pragma unroll
   for (int i = 0; i < kPasses; ++i)
     *reinterpret_cast<stage4*>(dst + (lrow + kRowsPerPass * i) * PITCH + lk) = reg[i];
@@ -184,15 +193,18 @@ __global__ __launch_bounds__(THREADS, kSplit ? 3 : 2) void msm_pair_min_kernel(
   load(false, min(2, nk - 1) * BK, rb0);
   __syncthreads();
 
+  // lane (lr, lh) reads segments lh and lh + 2 of rows wm*64 + lr (+ 32) and wn*64 + lr
+  // (+ 32): the row offsets are multiples of 16, so the swizzle is that of lr
+  const int seg_off[2] = {4 * (lh ^ seg_swizzle(lr)), 4 * ((lh + 2) ^ seg_swizzle(lr))};
   auto compute = [&](int buf) {
-    const float* A = smem + buf * kStage + (wm * 64 + lr) * PITCH + 4 * lh;
-    const float* B = smem + buf * kStage + BM * PITCH + (wn * 64 + lr) * PITCH + 4 * lh;
+    const float* A = smem + buf * kStage + (wm * 64 + lr) * PITCH;
+    const float* B = smem + buf * kStage + BM * PITCH + (wn * 64 + lr) * PITCH;
 #pragma unroll
     for (int s = 0; s < BK / 8; ++s) {
-      const float4 a0 = *reinterpret_cast<const float4*>(A + 8 * s);
-      const float4 a1 = *reinterpret_cast<const float4*>(A + 32 * PITCH + 8 * s);
-      const float4 b0 = *reinterpret_cast<const float4*>(B + 8 * s);
-      const float4 b1 = *reinterpret_cast<const float4*>(B + 32 * PITCH + 8 * s);
+      const float4 a0 = *reinterpret_cast<const float4*>(A + seg_off[s]);
+      const float4 a1 = *reinterpret_cast<const float4*>(A + 32 * PITCH + seg_off[s]);
+      const float4 b0 = *reinterpret_cast<const float4*>(B + seg_off[s]);
+      const float4 b1 = *reinterpret_cast<const float4*>(B + 32 * PITCH + seg_off[s]);
       const float av[2][4] = {{a0.x, a0.y, a0.z, a0.w}, {a1.x, a1.y, a1.z, a1.w}};
       const float bv[2][4] = {{b0.x, b0.y, b0.z, b0.w}, {b1.x, b1.y, b1.z, b1.w}};
 #pragma unroll
