@@ -123,10 +123,12 @@ int musc_msm_nearest_f32(const float* z, int n, int p, int c, float* nearest,
  *                different images, reduced along rows and columns into the
  *                per-(patch, image) minima (the hot kernel);
  *   refine       exact minima where ||a||^2 + ||b||^2 - 2 a.b cancels: every
- *                (patch, image) minimum with d^2 <= 32 FLT_EPSILON c (||q||^2 +
- *                the image's largest ||r||^2) is recomputed over that image's p
- *                patches by explicit differences, as the reference recomputes
- *                such pairs (models/modules/_MSM_gpu.py:219-228); with nothing to
+ *                (patch, image) minimum with d^2 <= max(32 c, 4096) FLT_EPSILON
+ *                (||q||^2 + the image's largest ||r||^2) is recomputed over that
+ *                image's p patches by explicit differences, as the reference
+ *                recomputes such pairs (models/modules/_MSM_gpu.py:219-228, bound
+ *                32 FLT_EPSILON c (||q||^2 + ||r||^2); the floor of 4096 covers the
+ *                norm roundings that bound misses for small c); with nothing to
  *                recompute it reads the minima once.  Works on the workspace of
  *                either engine (the split engine's included) after its
  *                pair_minima, with the same z;

@@ -313,20 +313,24 @@ __global__ __launch_bounds__(256) void msm_nearest_kernel(const uint32_t* __rest
 // root of that error: a few 1e-4 in d for unit rows.  The reference's accelerated MSM
 // recomputes every pair with d^2 <= 32 eps C (||q||^2 + ||r||^2) by explicit
 // differences (models/modules/_MSM_gpu.py:219-228).  Here one pass over the minima
-// keys flags each (row, image) minimum at or below 32 eps C (norms[row] + the largest
-// norm of the image) -- the same bound with the image's largest norm, so every pair
-// the reference recomputes lies in a flagged (row, image) or cannot be its minimum --
-// and the wave recomputes that minimum over all P patches of the image as
+// keys flags each (row, image) minimum at or below max(32 C, 4096) eps (norms[row] +
+// the largest norm of the image) -- the reference's bound with the image's largest
+// norm, so every pair the reference recomputes lies in a flagged (row, image) or
+// cannot be its minimum, and never below 4096 eps: the roundings of the two norms and
+// of the final sum leave ~3 eps (||q||^2 + ||r||^2) in d^2 whatever C is, which 32 eps C
+// does not cover for small C (at C = 3, minima just above it came out 2.2e-5 from the
+// exact value); above 4096 eps (||q||^2 + ||r||^2) they move d by at most ~1e-5 at C = 3
+// -- and the wave recomputes that minimum over all P patches of the image as
 // sum_c (s_a a_c - s_b b_c)^2 in fp32 (s the row scales: 1 / ||z|| with row
 // normalisation, else 1), accurate to a few ulps of d^2 itself; identical rows give
-// exactly 0.  Above the bound the expanded form's error in d is at most about
-// eps ||.||^2 / (2 d), far below the 2e-5 gate.  A flagged minimum is replaced
+// exactly 0.  For C >= 128 the bound is the reference's.  A flagged minimum is replaced
 // (stored), not merged: the exact value may lie above the expanded one.  NaN minima
 // (key 0), the own image and +inf (key kMinFill) are left alone.  With nothing
 // flagged the pass reads the keys once (37.7 MB at N = 83, P = 1369).
 // ---------------------------------------------------------------------------
 constexpr int kRefineRows = 16;                 // rows per wave
 constexpr float kRefineEps = 1.192092896e-7f;   // the fp32 machine epsilon of the reference's bound
+constexpr float kRefineFloor = 4096.f;          // smallest multiplier of eps (norm[q] + max norm[r])
 
 // Minimum over rows q in [q0, q1) of sum_c (s_row z_row,c - s_q z_q,c)^2, in every lane.
 // The products are rounded before the difference (no contraction), as the
@@ -446,7 +450,7 @@ int run_refine(const float* z, int n, int p, int c, const Workspace& w, hipStrea
   const long long rows = (long long)n * p;
   const long long blocks = ((rows + kRefineRows - 1) / kRefineRows + 3) / 4;
   hipLaunchKernelGGL(msm_refine_kernel, dim3((unsigned)blocks), dim3(256), 0, s, z, (int)rows, n, p, c, w.norms,
-                     w.scale, w.imgmax, w.minbits, 32.f * kRefineEps * (float)c);
+                     w.scale, w.imgmax, w.minbits, fmaxf(32.f * (float)c, kRefineFloor) * kRefineEps);
   return check_launch();
 }
 

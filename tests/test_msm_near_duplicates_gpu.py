@@ -19,8 +19,8 @@ from oracle import msm as om
 
 pytestmark = pytest.mark.gpu
 ATOL = 2e-5
-# planted distances: exact duplicates up to past the refinement bound (d^2 <= 32 eps C
-# (||q||^2 + ||r||^2) = 7.8e-3 for unit rows at C = 1024, i.e. d <= 0.088)
+# planted distances: exact duplicates up to past the refinement bound (d^2 <= max(32 C,
+# 4096) eps (||q||^2 + ||r||^2) = 7.8e-3 for unit rows at C = 1024, i.e. d <= 0.088)
 DELTAS = (0.0, 1e-7, 1e-6, 1e-5, 1e-4, 1e-3, 3e-3, 1e-2, 3e-2, 0.08, 0.1, 0.2)
 
 
