@@ -242,7 +242,9 @@ int musc_adaptive_pool_f32(const float* in, int batch, int side_in, int ch, int 
  *           (models/musc.py:259,263), upsampled bilinearly with align_corners=True
  *           (models/musc.py:269-272).
  * image_scores (n,) float64 out: max over each upsampled map (models/musc.py:288).
- *           May be NULL.  maps may be NULL when only image_scores are wanted. */
+ *           May be NULL.  maps may be NULL when only image_scores are wanted.
+ * Any out_size >= 1 (upsampling or downsampling); side <= 128 (MUSC_ERR_UNSUPPORTED
+ * beyond: a grid row is staged whole in LDS). */
 int musc_maps_f64(const double* scores, int n_radii, int n_layers, int n, int side,
                   int out_size, double* maps, double* image_scores,
                   hipStream_t stream);

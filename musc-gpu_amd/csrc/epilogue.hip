@@ -5,9 +5,11 @@
 // mean over radii, view (N, 1, side, side), F.interpolate(size=S, bilinear,
 // align_corners=True), image score = max of each S x S map.
 //
-// One workgroup per (image, band of kRows output rows).  A band touches at most
-// a few grid rows, so the workgroup averages only those rows of the n_radii *
-// n_layers score maps into LDS, then writes its kRows x S pixels (coalesced
+// One workgroup per (image, band of output rows: kRows when upsampling, fewer when a
+// strong downsampling would make kRows rows span more than kMaxGridRows grid rows,
+// down to one).  A band touches at most a few grid rows, so the workgroup averages
+// only those rows of the n_radii * n_layers score maps into LDS, then writes its
+// band of S-pixel rows (coalesced
 // float64 rows) and merges its band maximum into image_scores with a 64-bit
 // atomicMax on the bit pattern (all scores are non-negative distances, whose
 // IEEE bits order like the values).  The maximum propagates NaN, as numpy's max
@@ -18,7 +20,7 @@
 namespace musc {
 namespace epi {
 
-constexpr int kRows = 8;
+constexpr int kRows = 8;           // output rows per band at most
 constexpr int kThreads = 256;
 constexpr int kMaxSide = 128;
 constexpr int kMaxGridRows = 16;  // grid rows one band may touch
@@ -26,12 +28,13 @@ constexpr int kMaxGridRows = 16;  // grid rows one band may touch
 __device__ inline double nmax(double a, double b) { return __builtin_elementwise_maximum(a, b); }
 
 __global__ __launch_bounds__(kThreads) void maps_kernel(const double* __restrict__ scores, int n_radii, int n_layers,
-                                                        int n, int side, int out_size, double* __restrict__ maps,
+                                                        int n, int side, int out_size, int rows,
+                                                        double* __restrict__ maps,
                                                         unsigned long long* __restrict__ image_bits) {
-  const int bands = (out_size + kRows - 1) / kRows;
+  const int bands = (out_size + rows - 1) / rows;
   const int img = blockIdx.x / bands, band = blockIdx.x % bands;
-  const int y0 = band * kRows;
-  const int y1 = min(out_size, y0 + kRows);
+  const int y0 = band * rows;
+  const int y1 = min(out_size, y0 + rows);
   const int P = side * side;
   const double scale = out_size > 1 ? (double)(side - 1) / (double)(out_size - 1) : 0.0;
   // grid rows touched by output rows y0..y1-1
@@ -95,15 +98,17 @@ extern "C" int musc_maps_f64(const double* scores, int n_radii, int n_layers, in
   if (!scores || n_radii < 1 || n_layers < 1 || n < 1 || side < 1 || out_size < 1) return MUSC_ERR_INVALID_ARG;
   if (!maps && !image_scores) return MUSC_ERR_INVALID_ARG;
   if (side > epi::kMaxSide) return MUSC_ERR_UNSUPPORTED;
-  // a band of min(kRows, out_size) output rows touches at most floor(scale*(rows-1)) + 3 grid rows
+  // a band of R output rows starting at y0 touches grid rows floor(scale y0) ..
+  // floor(scale (y0 + R - 1)) + 1, at most floor(scale (R - 1)) + 3 of them: take the
+  // largest R <= kRows within kMaxGridRows (R = 1 always is: 3 rows)
   const double scale = out_size > 1 ? (double)(side - 1) / (double)(out_size - 1) : 0.0;
-  const int band_rows = out_size < epi::kRows ? out_size : epi::kRows;
-  if ((int)(scale * (band_rows - 1)) + 3 > epi::kMaxGridRows) return MUSC_ERR_UNSUPPORTED;
-  const int bands = (out_size + epi::kRows - 1) / epi::kRows;
+  int rows = epi::kRows;
+  while (rows > 1 && (int)(scale * (rows - 1)) + 3 > epi::kMaxGridRows) --rows;
+  const int bands = (out_size + rows - 1) / rows;
   if ((long long)n * bands > 0x7fffffffLL) return MUSC_ERR_UNSUPPORTED;
   unsigned long long* bits = reinterpret_cast<unsigned long long*>(image_scores);
   if (bits) launch_fill_u32(reinterpret_cast<uint32_t*>(bits), (size_t)n * 2, 0u, stream);
   hipLaunchKernelGGL(epi::maps_kernel, dim3((unsigned)(n * bands)), dim3(epi::kThreads), 0, stream, scores, n_radii,
-                     n_layers, n, side, out_size, maps, bits);
+                     n_layers, n, side, out_size, rows, maps, bits);
   return check_launch();
 }
