@@ -197,7 +197,12 @@ int musc_lnamd_workspace_bytes(int batch, int n_layers, size_t* out);
  *          of dtype in_dtype, contiguous.  When has_cls != 0 token 0 of each image
  *          is the class token and is skipped; the remaining tokens form a
  *          side x side grid (side*side == tokens_per_image - has_cls).
- * radii    host array of n_radii odd radii (1, 3, 5, ...; r <= side).
+ * radii    host array of n_radii odd radii (1, 3, 5, 7 or 9, in any order; a window
+ *          may exceed the grid); the output keeps the caller's order.
+ * Limits: n_radii <= 4, n_layers <= 16, 4 <= c <= 4096 with c % 4 == 0, a grid side
+ *          of at most 1024, and 32 * n_radii * side bytes of LDS (48 * n_radii * side
+ *          with pooling) within 64 KB: side <= 1024 for one or two radii, 682 for
+ *          three, 512 for four (341 pooled); MUSC_ERR_UNSUPPORTED beyond.
  * eps      LayerNorm epsilon (torch default 1e-5).
  * out      fp32, layout out_layout, batch*P*n_layers*c*n_radii floats.
  * Semantics per radius r and layer l (models/modules/_LNAMD.py:72-129 and the
@@ -256,7 +261,8 @@ int musc_maps_f64(const double* scores, int n_radii, int n_layers, int n, int si
  *   out          (n,) fp32: mean over k of sum_{j in top-k(i)} W_ij s_j / sum W_ij with
  *                W = X X^T and s the min-max normalised scores.
  * The reference returns the scores unchanged when k_list contains 0; callers do that
- * check (the entry point rejects k < 1). */
+ * check (the entry point rejects k < 1).  Limits: n <= 4096, n_k <= 16
+ * (MUSC_ERR_UNSUPPORTED beyond). */
 int musc_rscin_f32(const float* cls_tokens, const double* image_scores, int n, int d,
                    const int* k_list, int n_k, float* out, hipStream_t stream);
 
