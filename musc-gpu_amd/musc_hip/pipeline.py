@@ -47,8 +47,8 @@ def msm_all(pools: torch.Tensor, topmin_min: float = 0, topmin_max: float = 0.3,
             rank_events: list | None = None, refine_events: list | None = None) -> torch.Tensor:
     """(R, L, N, P) float64 MSM maps of every (radius, layer) pool.
 
-    Runs the three MSM stages explicitly (prepare, pair minima, rank) so that a
-    caller can pass `pair_events`, a list that receives one (start, end)
+    Runs the four MSM stages explicitly (prepare, pair minima, cancellation
+    refinement, rank) so that a caller can pass `pair_events`, a list that receives one (start, end)
     torch.cuda.Event pair recorded around each pair-minima kernel on the stream
     it runs on (`rank_events` and `refine_events` the same around each rank and
     cancellation-refinement kernel).  `engine` selects how the dot products are
