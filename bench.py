@@ -1,7 +1,8 @@
 """Benchmark: MuSc mutual scoring of the default pool on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config pool|plumbing]
-                    [--no-cpu-baseline] [--no-split] [--no-attention] [--cpu-full]
+                    [--no-cpu-baseline] [--no-split] [--no-attention] [--no-config3]
+                    [--no-config5] [--cpu-full]
 
 One step is one pass of the hot path over the whole synthetic pool, inputs
 resident in HBM: LNAMD for every (layer, radius) (window sums of x - mean), the
@@ -40,6 +41,16 @@ softmax(q k^T / 8) v; beside it, on the same fp16 inputs, the same products in
 torch ops (torch.bmm with torch's softmax, the math path, and with the
 reference's fp32-statistics softmax, its accelerated encoder's design), timed
 and checked the same way; `--no-attention` skips it.
+
+`super_fast_config3` and `e2e_config5` time BASELINE configs 3 and 5 with both MSM
+engines: config 3 (83 images, one layer, LNAMD r=3 with the 37 -> 28 pooling in the
+same pass, MSM on the 784-patch pool, the epilogue; median of `--steps` passes after
+the warm-up) and config 5 (the random-init ViT-L/14 at 518 px over 160 seeded images
+in batches of 4 under fp16 autocast, LNAMD r 1/3/5, 12 MSM calls, the epilogue and
+RsCIN; one warm-up and one timed pass per engine).  Each gates the split engine's maps
+and image scores (config 5: also RsCIN's scores) against the fp32 engine's at 2e-5;
+the fp32 engine itself is pinned against the oracle by the parity tests at these
+sizes.  `--no-config3` / `--no-config5` skip them.
 """
 from __future__ import annotations
 
@@ -469,6 +480,74 @@ def attention_config4(seed: int, iters: int = 3) -> dict:
     return out
 
 
+def _engine_agreement(ref: dict, got: dict) -> dict:
+    from musc_hip import agreement
+    out = {k: agreement.compare_arrays(ref[k].cpu(), got[k].cpu()) for k in ref}
+    out['pass'] = all(v['pass'] for v in out.values())
+    return out
+
+
+def super_fast_config3(seed: int, steps: int) -> dict:
+    """Config 3 (super_fast shape) with both MSM engines: images/s and agreement."""
+    import torch
+    from musc_hip import pipeline, synthetic
+
+    dev = torch.device('cuda:0')
+    n = 83
+    tokens = [synthetic.plumbing_tokens(n, 1370, 1024, seed=seed).to(dev)]
+    out = {'workload': 'config 3: N=83 x 1 layer, LNAMD r=3 with 37 -> 28 pooling fused, MSM P=784, ranks [0, 24), '
+                       'maps 518 x 518'}
+    res = {}
+    for engine in ('fp32', 'split16'):
+        ts = []
+        for it in range(steps + 1):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            maps, img = pipeline.score_pool(tokens, r_list=[3], image_size=518, pool_grid=28, msm_engine=engine)
+            e1.record()
+            torch.cuda.synchronize()
+            if it:
+                ts.append(e0.elapsed_time(e1))
+        ms = sorted(ts)[len(ts) // 2]
+        out[engine] = {'images_per_s': n / (ms / 1e3), 'median_ms_per_pass': ms, 'passes': steps}
+        res[engine] = {'maps': maps, 'image_scores': img}
+    out['agreement_split16_vs_fp32'] = _engine_agreement(res['fp32'], res['split16'])
+    return out
+
+
+def e2e_config5(seed: int) -> dict:
+    """Config 5 end to end (encoder, LNAMD, MSM, epilogue, RsCIN) with both MSM engines."""
+    import torch
+    from musc_hip import pipeline, synthetic, vit
+
+    dev = torch.device('cuda:0')
+    torch.manual_seed(0)
+    model = vit.vit_l14(518).to(dev).eval()
+    imgs, anomalous = synthetic.images(n=160, size=518, seed=seed)
+    imgs = imgs.to(dev)
+    out = {'workload': 'config 5: random-init ViT-L/14 at 518 px, N=160 seeded images (8 anomalous), batches of 4 '
+                       'under fp16 autocast, tokens after blocks 6/12/18/24, LNAMD r 1/3/5, 12 MSM calls (ranks '
+                       '[0, 47)), epilogue 518 x 518, RsCIN k=1,2,3',
+           'anomalous_images': anomalous}
+    res = {}
+    for engine in ('fp32', 'split16'):
+        for it in range(2):
+            timing = {}
+            r = pipeline.run_category(model, imgs, timing=timing, msm_engine=engine)
+            torch.cuda.synchronize()
+        e0, e1, e2, e3 = timing['events'][0]
+        total = e0.elapsed_time(e3)
+        out[engine] = {'images_per_s': 160 / (total / 1e3), 'ms': total, 'encoder_ms': e0.elapsed_time(e1),
+                       'lnamd_msm_epilogue_ms': e1.elapsed_time(e2), 'rscin_ms': e2.elapsed_time(e3)}
+        res[engine] = {'maps': r['maps'], 'image_scores': r['image_scores'],
+                       'rscin_scores': torch.as_tensor(r['scores']).double()}
+        del r
+    out['agreement_split16_vs_fp32'] = _engine_agreement(res['fp32'], res['split16'])
+    del model, imgs, res
+    torch.cuda.empty_cache()
+    return out
+
+
 def _fp32_stats_softmax(x):
     """Softmax over the last axis of fp16 logits with fp32 maximum and sum, P rounded to fp16
     (models/modules/_attention_gpu.py:41-81)."""
@@ -489,6 +568,8 @@ def main() -> int:
     ap.add_argument('--no-split', action='store_true',
                     help='skip the second measurement with the split (3x fp16 MFMA) MSM engine')
     ap.add_argument('--no-attention', action='store_true', help='skip the config-4 attention measurement')
+    ap.add_argument('--no-config3', action='store_true', help='skip the config-3 (super_fast) measurement')
+    ap.add_argument('--no-config5', action='store_true', help='skip the config-5 (end-to-end) measurement')
     ap.add_argument('--cpu-full', action='store_true',
                     help='also time the CPU restatement over the whole config-2 job (about six minutes)')
     args = ap.parse_args()
@@ -671,6 +752,24 @@ def main() -> int:
         except Exception as exc:  # noqa: BLE001
             result['attention_config4'] = {'error': repr(exc)}
             log(f'[bench] config-4 attention failed: {exc!r}')
+    if not args.no_config3 and args.config == 'pool':
+        try:
+            result['super_fast_config3'] = super_fast_config3(args.seed, args.steps)
+            c3 = result['super_fast_config3']
+            log(f"[bench] config 3: fp32 engine {c3['fp32']['images_per_s']:.0f}, split engine "
+                f"{c3['split16']['images_per_s']:.0f} images/s")
+        except Exception as exc:  # noqa: BLE001
+            result['super_fast_config3'] = {'error': repr(exc)}
+            log(f'[bench] config 3 failed: {exc!r}')
+    if not args.no_config5 and args.config == 'pool':
+        try:
+            result['e2e_config5'] = e2e_config5(args.seed)
+            c5 = result['e2e_config5']
+            log(f"[bench] config 5: fp32 engine {c5['fp32']['images_per_s']:.1f}, split engine "
+                f"{c5['split16']['images_per_s']:.1f} images/s")
+        except Exception as exc:  # noqa: BLE001
+            result['e2e_config5'] = {'error': repr(exc)}
+            log(f'[bench] config 5 failed: {exc!r}')
     if not args.no_cpu_baseline:
         log('[bench] timing the CPU baseline (oracle restatement, bounded sample) and checking agreement')
         pools = pipeline.lnamd_pools(tokens, r_list)
