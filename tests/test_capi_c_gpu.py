@@ -1,5 +1,7 @@
 """The C-ABI from plain C: tests/capi_c/msm_from_c.c links libmusc_hip.so and the HIP
-runtime (no Python, no torch) and checks musc_msm_scores_f32 against a float64 brute force."""
+runtime (no Python, no torch), checks musc_msm_scores_f32 against a float64 brute force, the
+four MSM stages called one by one and the no-allocation entry point against it bit for bit,
+the split engine's P >= 256 rejection and the epilogue at identity size."""
 import os
 import subprocess
 
