@@ -21,12 +21,17 @@ softmax.  Here, for the duration of the call, the forward of every block in
   out-projection.
 
 The tower's ln_pre and ln_post (the same cast-back LayerNorm) are swapped for the
-one-pass kernel too, and the patch embedding conv1 (transformer.py:380, :566: a
-Conv2d whose kernel equals its stride) becomes what it computes, a GEMM of the
-image's non-overlapping patches: one gather of the patches into (B * grid^2,
-3 * p^2) rows in the compute dtype, then torch's GEMM (hipBLASLt).  The convolution
-library chooses its algorithm per shape and, without a tuned database, can fall
-back to a direct convolution 60x slower than the GEMM.
+one-pass kernel too.  The patch embedding conv1 (transformer.py:380, :566: a Conv2d
+whose kernel equals its stride) keeps the model's own convolution by default, the
+one the math path runs: under fp16 autocast the convolution library's result and an
+fp32-accumulated GEMM of the same patches round differently in over half of the
+outputs, a difference the following blocks carry to every token (on the ViT-L/14 of
+BASELINE config 5 with its weights scaled by 1/4 it alone moves the anomaly maps by
+2.3e-5, where the fused blocks without it stay within 5.2e-6 of the math path), for
+2 ms per 160 images.  Setting PATCH_EMBED_GEMM = True replaces conv1 by what it
+computes, a GEMM of the image's non-overlapping patches (one gather of the patches
+into (B * grid^2, 3 * p^2) rows in the compute dtype, then torch's GEMM), for
+setups whose convolution library falls back to a slow direct kernel.
 
 Only block 12, whose weights Transformer.forward keeps (transformer.py:331-333),
 also returns head-averaged probabilities (musc_attention_weights_strided); other
@@ -52,6 +57,9 @@ from ._aggregation_cache import RadiusAggregationCache
 from ._lnamd_hip import aggregate_features
 
 _STATS = {}
+
+# conv1 as a patch GEMM (see the module docstring); off: the model's own convolution
+PATCH_EMBED_GEMM = False
 
 
 def begin_inference():
@@ -222,7 +230,7 @@ def encode_image(model, image, out_layers):
                 restored.append((ln, 'forward' in ln.__dict__, ln.__dict__.get('forward')))
                 ln.forward = _fused_ln_forward(ln, ln.forward)
         conv1 = getattr(visual, 'conv1', None)
-        if _patch_conv(conv1):
+        if PATCH_EMBED_GEMM and _patch_conv(conv1):
             restored.append((conv1, 'forward' in conv1.__dict__, conv1.__dict__.get('forward')))
             conv1.forward = _patch_embed_forward(conv1, conv1.forward)
         for index, block in enumerate(blocks):

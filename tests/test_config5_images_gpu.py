@@ -34,7 +34,9 @@ with its fused attention replaced by the same restatement (the math path's round
 points: fp16 logits, fp32 max and sum, P = fp16(exp(l - max) / sum), fp16 P.V): the
 maps then move by as much as the product's own do, so aligning the attention's
 rounding points does not bring the fp16 comparison under 2e-5 either -- the
-LayerNorm and patch-embedding reduction orders alone move them that far.
+one-pass LayerNorm's reduction order alone moves them that far on this model.  With
+the same model's weight matrices scaled by 1/4, whose blocks damp rounding
+differences, the product meets the 2e-5 gate from images (last test).
 """
 import numpy as np
 import pytest
@@ -235,3 +237,45 @@ def test_config5_fp16_from_images_within_reference_design_spread(setup, monkeypa
     print(f'config5 fp16 from images, product path with the reference design attention: maps {em:.3e}, '
           f'image scores {ei:.3e}', flush=True)
     assert em <= gate[0] and ei <= gate[1]
+
+
+def test_config5_fp16_from_images_at_quarter_weight_scale(setup):
+    # The same architecture and images with every weight matrix scaled by 1/4: its blocks
+    # damp rounding differences instead of amplifying them (the reference design's own
+    # distance from the math path falls from 3.0e-5 to 4.6e-6, near the 4.3e-6 the
+    # reference reports for its real-weight encoder, benchmarks/representative/REPORT.md:38),
+    # so here the product must meet the reference's 2e-5 gate from images under fp16
+    # autocast, both engines.  The scaled encoder's class tokens all but coincide (their
+    # neighbour gaps lie below the paths' similarity differences), so RsCIN is checked
+    # against the definition on the product's own inputs, and against the math path on
+    # the rows whose neighbours are stable, if any
+    _, imgs = setup
+    torch.manual_seed(0)
+    model = vit.vit_l14(518).eval().to(imgs.device)
+    with torch.no_grad():
+        for prm in model.parameters():
+            if prm.ndim >= 2:
+                prm.mul_(0.25)
+    ref_tok, ref_cls = _encode_math(model, imgs, autocast=True)
+    ref_maps, ref_img = _oracle_chain(ref_tok)
+    out = pipeline.run_category(model, imgs, feature_layers=LAYERS, r_list=R_LIST, batch_size=4, k_list=K_LIST,
+                                autocast=True)
+    print(f'config5 fp16 at weight scale 1/4, product tokens vs math path: {_token_drift(out["tokens"], ref_tok)}',
+          flush=True)
+    del ref_tok
+    split_maps, split_img = pipeline.score_pool(out['tokens'], r_list=R_LIST, image_size=518, msm_engine='split16')
+    for what, maps, img in (('fp32 engine', out['maps'], out['image_scores']), ('split16 engine', split_maps, split_img)):
+        em, ei = _max_err(maps, ref_maps), _max_err(img, ref_img)
+        print(f'config5 fp16 at weight scale 1/4 ({what}): maps {em:.3e}, image scores {ei:.3e}', flush=True)
+        assert em <= ATOL and ei <= ATOL
+    got = out['scores'].cpu().numpy().astype(np.float64)
+    ref = orc.rscin_bruteforce_f64(ref_img.numpy(), ref_cls.cpu().numpy(), list(K_LIST))
+    stable, delta = _stable_rows(ref_cls, out['class_tokens'], K_LIST)
+    err = np.abs(got - ref)
+    print(f'config5 fp16 at weight scale 1/4, RsCIN: similarities differ by {delta:.2e}; {int(stable.sum())} of '
+          f'{len(stable)} rows keep the same neighbours, worst {err[stable].max() if stable.any() else 0.0:.3e}',
+          flush=True)
+    assert np.all(err[stable] <= ATOL)
+    ok, info = orc.check_rscin(got, out['image_scores'].cpu().numpy(), out['class_tokens'].cpu().numpy(),
+                               list(K_LIST), atol=ATOL)
+    assert ok, info

@@ -14,7 +14,9 @@ def small_model(device, layers=4):
     return m.to(device).eval()
 
 
-def test_fp32_tokens_match_math_path(device):
+@pytest.mark.parametrize('patch_gemm', [False, True])
+def test_fp32_tokens_match_math_path(device, monkeypatch, patch_gemm):
+    monkeypatch.setattr(_encoder_hip, 'PATCH_EMBED_GEMM', patch_gemm)
     model = small_model(device)
     image = torch.rand((2, 3, 56, 56), generator=torch.Generator().manual_seed(1)).to(device)
     with torch.no_grad():
@@ -28,7 +30,7 @@ def test_fp32_tokens_match_math_path(device):
     stats = _encoder_hip.research_diagnostics()
     assert stats['fused_blocks'] == 4 and stats['fused_attention_calls'] == 4 and stats['weight_blocks'] == 1
     assert stats['fused_layer_norms'] == 2 and stats['fallback_calls'] == 0        # ln_pre, ln_post
-    assert stats['patch_embeds'] == 1
+    assert stats['patch_embeds'] == (1 if patch_gemm else 0)
     # the original forwards are restored
     for blk in model.visual.transformer.resblocks:
         assert 'forward' not in blk.__dict__ and 'forward' not in blk.attn.__dict__

@@ -233,8 +233,8 @@ def test_nan_aware_match():
 
 def test_patch_embedding_hook_predicate_and_cpu_fallback():
     # conv1 (kernel == stride, no padding / dilation / groups) is what the encoding plugin
-    # turns into patches @ W^T; anything else, and any input the GEMM path does not take
-    # (here: a CPU tensor), keeps the module's own forward
+    # turns into patches @ W^T when PATCH_EMBED_GEMM is set; anything else, and any input
+    # the GEMM path does not take (here: a CPU tensor), keeps the module's own forward
     from musc_hip import _encoder_hip
     conv = torch.nn.Conv2d(3, 16, kernel_size=14, stride=14, bias=False)
     assert _encoder_hip._patch_conv(conv)
