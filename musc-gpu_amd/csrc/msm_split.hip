@@ -21,21 +21,24 @@
 //
 // MI355X layout
 //   split array   per row, per 16-channel block: hi[16] | lo[16] fp16 (64 bytes, one
-//                 row's share of a pipeline stage); channels padded to a multiple of
-//                 16 with zeros.
+//                 row's share of a pipeline stage); channels padded with zeros to a
+//                 whole number of 32-channel pairs of blocks.
 //   pair kernel   256 x 256 tiles of the upper triangle (symmetric reuse, bands of
-//                 8 tile rows, XCD-grouped); a workgroup takes one 128-row half, two
-//                 workgroups share a CU, 4 waves each own 64 x 128.  Stages of 16
-//                 channels go straight from global memory into LDS
-//                 (buffer_load_dwordx4 ... lds: lane l of a load lands at base + 16 l,
-//                 so one load fills 16 rows of 64 bytes) through a 3-deep ring, loads
-//                 2 stages ahead of the MFMAs, one barrier per stage, no staging
-//                 registers.  The 16-byte segment s of staged row r sits at position
-//                 s ^ ((r >> 2) & 3), which keeps the MFMA operand reads free of bank
-//                 conflicts.
-//                 Register epilogues as in the fp32 kernel (one image segment per
-//                 dimension, or two when the tile straddles an image boundary:
-//                 p >= 256 is required).
+//                 8 tile rows, XCD-grouped), one workgroup per tile and CU, 4 waves
+//                 each own 128 x 128 (accumulators in AGPRs).  Stages of 16 channels
+//                 (32 KB: 256 A rows + 256 B rows) go straight from global memory into
+//                 LDS (buffer_load_dwordx4 ... lds: lane l of a load lands at base +
+//                 16 l, so one load fills 16 rows of 64 bytes) through a 4-deep ring,
+//                 loads 4 stages ahead, one barrier per stage, no staging registers;
+//                 the next stage's operands are read into a second register set, and
+//                 the loads and reads are interleaved with the 48 MFMAs of a stage, so
+//                 that the one wave per SIMD keeps the matrix pipe fed.  The 16-byte
+//                 segment s of staged row r sits at position s ^ ((r >> 2) & 3), which
+//                 keeps the MFMA operand reads free of bank conflicts.
+//                 Register epilogues: tiles of one image pair fold each distance into
+//                 the row and column minima at once; tiles that straddle an image
+//                 boundary (p >= 256: one at most per dimension) keep the minima per
+//                 image segment, 64 rows at a time.
 #include <hip/hip_fp16.h>
 
 #include "msm_common.hpp"
@@ -46,23 +49,25 @@ namespace split {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 
-constexpr int TM = 256;                      // triangle tile: rows = columns
-constexpr int TR = 128;                      // tile rows per workgroup (half a triangle tile)
-constexpr int TC = 256;                      // tile columns per workgroup
+constexpr int TM = 256;                      // triangle tile: rows = columns, one workgroup per tile
 constexpr int KB = 16;                       // channels per stage (each of hi and lo)
 constexpr int ROWB = 4 * KB;                 // bytes per row and stage: hi[16] lo[16] fp16
-constexpr int NSTAGE = 3;                    // LDS ring depth: loads run NSTAGE - 1 stages ahead
-constexpr int THREADS = 256;                 // 4 waves: 2 (rows) x 2 (columns) of 64 x 128
-constexpr int kStageRows = TR + TC;          // A rows then B rows
-constexpr int kStageBytes = kStageRows * ROWB;  // 24 KB
+constexpr int NSTAGE = 4;                    // LDS ring depth: loads run NSTAGE stages ahead of the MFMAs
+constexpr int THREADS = 256;                 // 4 waves: 2 (rows) x 2 (columns) of 128 x 128
+constexpr int kWaveTile = 128;               // rows (and columns) per wave
+constexpr int kBlocks = kWaveTile / 32;      // 32 x 32 MFMA blocks per wave dimension
+constexpr int kStageRows = 2 * TM;           // A rows (tile rows) then B rows (tile columns)
+constexpr int kStageBytes = kStageRows * ROWB;  // 32 KB
 constexpr int kScaleShift = 10;              // normalised rows are scaled by 2^10
 constexpr int kBandSplit = BAND;             // tile rows per band of the triangle enumeration
-constexpr int kRowsPerLoad = kWave * 16 / ROWB;                          // 16 staged rows per direct load
-constexpr int kLoads = kStageRows / kRowsPerLoad / (THREADS / kWave);    // direct loads per wave per stage
+constexpr int kRowsPerLoad = kWave * 16 / ROWB;              // 16 staged rows per direct load
+constexpr int kWaveRows = kStageRows / (THREADS / kWave);    // 128 staged rows per wave and stage
+constexpr int kLoads = kWaveRows / kRowsPerLoad;             // direct loads per wave per stage
 
-static_assert(kLoads == 6, "stage loads: 384 rows, 16 per load, over 4 waves (the vmcnt(6) of the main loop)");
-static_assert(NSTAGE == 3, "the vmcnt waits of the main loop are written for a 3-deep ring");
-static_assert(THREADS == TC && TR <= THREADS, "the prologue and the final merge map thread t to column t");
+static_assert(kLoads == 8, "the vmcnt waits of the main loop count 8 loads per wave and stage");
+static_assert(NSTAGE == 4, "the vmcnt waits of the main loop are written for a 4-deep ring");
+static_assert(THREADS == TM, "the prologue and the final merge map thread t to tile row t and column t");
+static_assert(TM % kWaveRows == 0, "a wave's staged rows lie in one panel");
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef int int4v __attribute__((ext_vector_type(4)));
@@ -139,74 +144,74 @@ __global__ __launch_bounds__(256) void split_prepare_kernel(const float* __restr
 }
 
 // ---------------------------------------------------------------------------
-// Pair minima.  Workgroup w takes half (w & 1) -- 128 rows x all 256 columns -- of
-// triangle tile (w >> 1); two workgroups share a CU, so one's barrier and LDS-read
-// bubbles are covered by the other's MFMAs.
+// Pair minima.  Workgroup w takes triangle tile w (256 x 256), one workgroup per CU;
+// wave (wm, wn) owns tile rows wm*128 .. +127 x columns wn*128 .. +127, 4 x 4 blocks of
+// 32 x 32 accumulated in registers (AGPRs).  The operands of stage j+1 are read from
+// LDS into a second register set while the MFMAs of stage j run, so the single wave
+// per SIMD keeps issuing MFMAs; the 4-deep LDS ring holds loads up to four stages
+// ahead.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* __restrict__ hl,
+struct SplitOps {
+  half8 ahi[kBlocks], alo[kBlocks], bhi[kBlocks], blo[kBlocks];
+};
+
+__global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* __restrict__ hl,
                                                                const float* __restrict__ norms,
                                                                const float* __restrict__ inv,
                                                                uint32_t* __restrict__ minbits, int rows, int n, int p,
                                                                int nkb, int T, long long ntiles) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[NSTAGE * kStageBytes];
-  __shared__ __attribute__((aligned(16))) float s_rnorm[TR];
-  __shared__ __attribute__((aligned(16))) float s_rinv[TR];
-  __shared__ __attribute__((aligned(16))) int s_rimg[TR];
-  __shared__ float s_cnorm[TC];
-  __shared__ float s_cinv[TC];
-  __shared__ int s_cimg[TC];
+  __shared__ __attribute__((aligned(16))) float s_rnorm[TM];
+  __shared__ __attribute__((aligned(16))) float s_rinv[TM];
+  __shared__ float s_cnorm[TM];
+  __shared__ float s_cinv[TM];
 
   const long long w = xcd_logical_id(blockIdx.x, gridDim.x);
-  if (w >= 2 * ntiles) return;
-  const int2 tile = decode_tile<kBandSplit>(w >> 1, T);
-  const int row0 = tile.x * TM + (int)(w & 1) * TR, col0 = tile.y * TM;
-  if (row0 >= rows) return;  // lower half of a last tile row that lies in padding
-  const int rlast = min(row0 + TR, rows) - 1, clast = min(col0 + TC, rows) - 1;
+  if (w >= ntiles) return;
+  const int2 tile = decode_tile<kBandSplit>(w, T);
+  const int row0 = tile.x * TM, col0 = tile.y * TM;
+  const int rlast = min(row0 + TM, rows) - 1, clast = min(col0 + TM, rows) - 1;
   const int rimg0 = row0 / p, cimg0 = col0 / p;
-  const bool simple = (row0 + TR <= rows) && (col0 + TC <= rows) && (rlast / p == rimg0) && (clast / p == cimg0);
+  // simple: the tile's rows lie in one image and its columns in one image (no boundary,
+  // no padding); a tile of one image only has no pair to score
+  const bool simple = (row0 + TM <= rows) && (col0 + TM <= rows) && (rlast / p == rimg0) && (clast / p == cimg0);
   if (simple && rimg0 == cimg0) return;
 
-  const int t = threadIdx.x;  // THREADS == TC: thread t stages column t and, for t < TR, row t
+  const int t = threadIdx.x;  // THREADS == TM: thread t stages tile row t and tile column t
   {
-    const int cc = col0 + t;
+    const int r = row0 + t, cc = col0 + t;
+    s_rnorm[t] = r < rows ? norms[r] : 0.f;
+    s_rinv[t] = r < rows ? -2.f * inv[r] : 0.f;  // -2 x row scale (exact)
     s_cnorm[t] = cc < rows ? norms[cc] : 0.f;
     s_cinv[t] = cc < rows ? inv[cc] : 0.f;
-    s_cimg[t] = cc < rows ? cc / p : n;  // n marks "no image" (padding)
-    if (t < TR) {
-      const int r = row0 + t;
-      s_rnorm[t] = r < rows ? norms[r] : 0.f;
-      s_rinv[t] = r < rows ? -2.f * inv[r] : 0.f;  // -2 x row scale (exact)
-      s_rimg[t] = r < rows ? r / p : n;
-    }
   }
 
   const int wave = t / kWave, lane = t % kWave;
   const int wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
 
-  floatx16 acc[2][4];
+  floatx16 acc[kBlocks][kBlocks];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < kBlocks; ++a)
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int b = 0; b < kBlocks; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.f;
 
   // Loads go straight from global memory into LDS (buffer_load_dwordx4 ... lds: lane
   // l of a load lands at M0 + 16 l, so one load fills 16 staged rows of 64 bytes).
-  // Wave wv fills staged rows wv*96 .. wv*96 + 95; staged rows 0..127 are tile rows
-  // (A), 128..383 tile columns (B).  Lane l of a load carries row R = R0 + l/4 into
-  // LDS position l % 4, i.e. segment (l % 4) ^ ((R >> 2) & 3).  Padded rows re-read
-  // the last row (masked in the epilogue).
-  // Addressing: two buffer resources, one based at the first row of the A panel and
-  // one at the first row of the B panel (64-bit bases, so the split array may have any
-  // size; each extent ends with its panel's last row), one 32-bit byte offset per load
-  // within its panel (row + segment, loop-invariant) and the stage offset as the scalar
-  // offset.  A load's 16 staged rows lie all in A or all in B (128 = 8 loads of 16
-  // rows), so each load names one resource.  The loads are issued from inline
-  // assembly so that the compiler, which cannot tell the ring buffers apart, does
-  // not wait for them before reading another buffer; the loop waits for them
-  // explicitly.
+  // Wave wv fills staged rows wv*128 .. wv*128 + 127: waves 0 and 1 the tile rows (A
+  // panel), waves 2 and 3 the tile columns (B panel).  Lane l of a load carries row
+  // R = R0 + l/4 into LDS position l % 4, i.e. segment (l % 4) ^ ((R >> 2) & 3).
+  // Padded rows re-read the last row (their pairs are masked in the epilogue).
+  // Addressing: one buffer resource per wave, based at the first row of its panel
+  // (64-bit base, so the split array may have any size; the extent ends with the
+  // panel's last row), one 32-bit byte offset per load within the panel (row +
+  // segment, loop-invariant) and the stage offset as the scalar offset.  The loads are
+  // issued from inline assembly so that the compiler, which cannot tell the ring
+  // buffers apart, does not wait for them before reading another buffer; the loop
+  // waits for them explicitly.
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
   const int lrow = lane >> 2;
   auto panel_rsrc = [&](int first, int last) {
     const unsigned long long addr =
@@ -218,32 +223,46 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
     r.w = kBufferFlags;
     return r;
   };
-  const int4v rsrcA = panel_rsrc(row0, rlast), rsrcB = panel_rsrc(col0, clast);
-  constexpr int kWaveRows = kStageRows / (THREADS / kWave);
-  static_assert(TR % kRowsPerLoad == 0, "a load's staged rows lie in one panel");
+  const bool waveA = wv * kWaveRows < TM;  // wave-uniform
+  const int4v rsrc = waveA ? panel_rsrc(row0, rlast) : panel_rsrc(col0, clast);
   uint32_t voff[kLoads];
 #pragma unroll
   for (int i = 0; i < kLoads; ++i) {
     const int R = wave * kWaveRows + i * kRowsPerLoad + lrow;
-    const int prow = R < TR ? min(R, rlast - row0) : min(R - TR, clast - col0);
+    const int prow = R < TM ? min(R, rlast - row0) : min(R - TM, clast - col0);
     const int lseg = (lane & 3) ^ ((R >> 2) & 3);
     voff[i] = (uint32_t)prow * (uint32_t)(nkb * ROWB) + (uint32_t)(lseg * 16);
   }
-  const uint32_t lds0 = (uint32_t)(size_t)(lds_void*)smem;
-  auto issue = [&](int kb, int buf) {
+  // wave-uniform LDS base of this wave's staged rows in buffer 0 (M0 is a scalar register)
+  const uint32_t lds_wave =
+      __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(lds_void*)smem + (uint32_t)(wv * kWaveRows * ROWB));
+  // load i (0 .. kLoads-1) of this wave's share of stage kb into LDS buffer buf
+  auto issue_one = [&](int kb, int buf, int i) {
     const uint32_t soff = (uint32_t)(kb * ROWB);
+    const uint32_t base = lds_wave + (uint32_t)(buf * kStageBytes);
+    // M0 = base + this load's 16 rows; s_nop: one wait state between the scalar write
+    // of M0 and the load that reads it
+    asm volatile("s_add_u32 m0, %0, %4\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(base), "v"(voff[i]), "s"(rsrc), "s"(soff), "i"(i * kRowsPerLoad * ROWB)
+                 : "memory", "m0", "scc");
+  };
+  auto issue = [&](int kb, int buf) {
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-      // wave-uniform LDS base of this load (M0 is a scalar register)
-      const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-          lds0 + (uint32_t)(buf * kStageBytes + (wave * kWaveRows + i * kRowsPerLoad) * ROWB));
-      // s_nop: one wait state between the scalar write of M0 and the load that reads it
-      const bool inA = __builtin_amdgcn_readfirstlane(wave * kWaveRows + i * kRowsPerLoad) < TR;  // wave-uniform
-      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                   :
-                   : "s"(m0), "v"(voff[i]), "s"(inA ? rsrcA : rsrcB), "s"(soff)
-                   : "memory", "m0");
-    }
+    for (int i = 0; i < kLoads; ++i) issue_one(kb, buf, i);
+  };
+  // Waits until this thread's loads of stage `st` have landed, given that the loads of
+  // every stage up to `last_issued` have been issued (loads complete in order).
+  auto wait_stage = [&](int st, int last_issued) {
+    const int later = last_issued - st;
+    if (later >= 3)
+      asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+    else if (later == 2)
+      asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if (later == 1)
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   };
   // Segments of a staged row: 0, 1 = hi channels 0-7, 8-15; 2, 3 = lo.  Segment s of
   // staged row r sits at position s ^ ((r >> 2) & 3); the operand rows here are
@@ -252,115 +271,140 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
   // 16 distinct 16-byte slots of a 256-byte bank window: conflict-free reads.
   const int sw = (lr >> 2) & 3;
   const int phi = (lh ^ sw) * 16, plo = ((2 + lh) ^ sw) * 16;
-  auto compute = [&](int buf) {
-    const unsigned char* As = smem + buf * kStageBytes + (wm * 64 + lr) * ROWB;
-    const unsigned char* Bs = smem + buf * kStageBytes + (TR + wn * 128 + lr) * ROWB;
-    half8 ahi[2], alo[2], bhi[4], blo[4];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      ahi[mb] = *reinterpret_cast<const half8*>(As + mb * 32 * ROWB + phi);
-      alo[mb] = *reinterpret_cast<const half8*>(As + mb * 32 * ROWB + plo);
-    }
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      bhi[nb] = *reinterpret_cast<const half8*>(Bs + nb * 32 * ROWB + phi);
-      blo[nb] = *reinterpret_cast<const half8*>(Bs + nb * 32 * ROWB + plo);
-    }
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
-        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[mb], bhi[nb], acc[mb][nb], 0, 0, 0);
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
-        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[mb], blo[nb], acc[mb][nb], 0, 0, 0);
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
-        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo[mb], bhi[nb], acc[mb][nb], 0, 0, 0);
+  const int aoff = (wm * kWaveTile + lr) * ROWB, boff = (TM + wn * kWaveTile + lr) * ROWB;
+  // operand vector r (0 .. 15) of stage buffer buf: block r / 4, one of A hi, A lo,
+  // B hi, B lo by r % 4
+  auto read_one = [&](int buf, SplitOps& o, int r) {
+    const int b = r >> 2, kind = r & 3;
+    const unsigned char* base = smem + buf * kStageBytes + (kind < 2 ? aoff : boff) + b * 32 * ROWB;
+    const half8 x = *reinterpret_cast<const half8*>(base + ((kind & 1) ? plo : phi));
+    if (kind == 0) o.ahi[b] = x;
+    if (kind == 1) o.alo[b] = x;
+    if (kind == 2) o.bhi[b] = x;
+    if (kind == 3) o.blo[b] = x;
   };
+  auto read_ops = [&](int buf, SplitOps& o) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) read_one(buf, o, r);
+  };
+  // MFMA idx (0 .. 47) of a stage: product idx / 16 (hi.hi, hi.lo, lo.hi), block
+  // (mb, nb) = ((idx % 16) / 4, idx % 4); per accumulator: hi.hi, then hi.lo, then lo.hi
+  auto mfma_one = [&](const SplitOps& o, int idx) {
+    const int prod = idx >> 4, mb = (idx >> 2) & 3, nb = idx & 3;
+    const half8 a = prod == 2 ? o.alo[mb] : o.ahi[mb];
+    const half8 b = prod == 1 ? o.blo[nb] : o.bhi[nb];
+    acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[mb][nb], 0, 0, 0);
+  };
+  using F = std::false_type;
+  using Tr = std::true_type;
 
-  // Stage kc lives in LDS buffer kc % NSTAGE and its loads go out NSTAGE - 1 stages
-  // ahead.  Iteration kc waits until this thread's loads of stage kc have landed
-  // (loads complete in order, so only the next stage's kLoads may still be in
-  // flight); the barrier then makes every wave's loads visible and guarantees that
-  // buffer (kc - 1) % NSTAGE is no longer read (compute(kc - 1) is done everywhere),
-  // so the loads of stage kc + NSTAGE - 1 can refill it.
-  for (int st = 0; st < NSTAGE - 1 && st < nkb; ++st) issue(st, st);
-  for (int kc = 0; kc < nkb; ++kc) {
-    if (kc + 1 < nkb)
-      asm volatile("s_waitcnt vmcnt(6)" ::: "memory");  // the next stage's kLoads may be in flight
-    else
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // Stage j lives in LDS buffer j % NSTAGE.  Step j: wait for this thread's loads of
+  // stage j + 1; the barrier then makes every wave's loads of stage j + 1 visible and
+  // guarantees that every wave has finished reading stage j (its reads completed before
+  // the barrier; its operands are in registers), so buffer j % NSTAGE takes the loads of
+  // stage j + NSTAGE; then the MFMAs of stage j run from registers while the operands of
+  // stage j + 1 are read into the other register set.  The last step reads a stale
+  // buffer into registers it never uses.  nkb is even (the split array is padded to
+  // whole pairs of stages), so the loop takes two steps per iteration with the two
+  // register sets in fixed roles.
+  for (int st = 0; st < NSTAGE && st < nkb; ++st) issue(st, st);
+  wait_stage(0, min(NSTAGE, nkb) - 1);
+  __syncthreads();
+  SplitOps o0, o1;
+  read_ops(0, o0);
+  // Within a step the 48 MFMAs go in 8 groups of 6, each group preceded by one direct
+  // load of stage j + NSTAGE (steps that have one) and two operand reads of stage j + 1,
+  // with scheduling barriers between the groups: with one wave per SIMD nothing else
+  // covers a load whose issue stalls or a read's latency, so they overlap the MFMAs
+  // already in the matrix pipe.
+  auto step = [&](int j, const SplitOps& cur, SplitOps& nxt, auto with_loads) {
+    wait_stage(j + 1, min(j + NSTAGE - 1, nkb - 1));
     __syncthreads();
-    if (kc + NSTAGE - 1 < nkb) issue(kc + NSTAGE - 1, (kc + NSTAGE - 1) % NSTAGE);
-    compute(kc % NSTAGE);
+#pragma unroll
+    for (int gi = 0; gi < kLoads; ++gi) {
+      if constexpr (decltype(with_loads)::value) issue_one(j + NSTAGE, j % NSTAGE, gi);
+      read_one((j + 1) % NSTAGE, nxt, 2 * gi);
+      read_one((j + 1) % NSTAGE, nxt, 2 * gi + 1);
+#pragma unroll
+      for (int k = 0; k < 6; ++k) mfma_one(cur, gi * 6 + k);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // j even and nkb even: j + NSTAGE < nkb also gives j + 1 + NSTAGE < nkb
+  int j = 0;
+  for (; j + NSTAGE < nkb; j += 2) {
+    step(j, o0, o1, Tr{});
+    step(j + 1, o1, o0, Tr{});
+  }
+  for (; j < nkb; j += 2) {
+    step(j, o0, o1, F{});
+    step(j + 1, o1, o0, F{});
   }
 
-  // Epilogue.  Lane (lr, lh) of wave (wm, wn) holds, for mb < 2, nb < 4, v < 16, the
-  // dot of tile row wm*64 + mb*32 + (v/4)*8 + lh*4 + v%4 with tile column
+  // Epilogue.  Lane (lr, lh) of wave (wm, wn) holds, for mb, nb < 4, v < 16, the dot
+  // of tile row wm*128 + mb*32 + (v/4)*8 + lh*4 + v%4 with tile column
   // wn*128 + nb*32 + lr.
-  const float inf = __int_as_float(kInfBits);
   const int rA = rimg0, cA = cimg0;
-  float d2[2][4][16];
+  const int wc0 = wn * kWaveTile;
+  const float inf = __int_as_float(kInfBits);
+  float cn[kBlocks], ci[kBlocks];
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int i0 = wm * 64 + mb * 32 + g * 8 + lh * 4;
-      const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[i0]);
-      const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[i0]);
-      const float rv[4] = {rn.x, rn.y, rn.z, rn.w};
-      const float rs[4] = {ri.x, ri.y, ri.z, ri.w};
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        const int j = wn * 128 + nb * 32 + lr;
-        const float cn = s_cnorm[j];
-        const float ci = s_cinv[j];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)  // clamped at 0 by min_key, after the minima
-          d2[mb][nb][g * 4 + e] = fmaf(rs[e] * ci, acc[mb][nb][g * 4 + e], rv[e] + cn);
-      }
-    }
+  for (int nb = 0; nb < kBlocks; ++nb) {
+    cn[nb] = s_cnorm[wc0 + nb * 32 + lr];
+    ci[nb] = s_cinv[wc0 + nb * 32 + lr];
+  }
 
-  if (simple) {
-    // column minima over this wave's 64 rows; the two lane halves then split the
-    // column blocks: half lh keeps blocks 2q + lh (q = 0, 1)
-    float cmin[4];
+  if (__builtin_expect(simple, 1)) {  // about two thirds of the tiles at P = 1369
+    // Rows of image rA, columns of image cA: each squared distance is formed and folded
+    // at once into the column minima (per nb, over this lane's rows) and the
+    // row-minimum items (per row, over this lane's columns), one 64-row half at a time.
+    const int wr0 = wm * kWaveTile;
+    float cmin[kBlocks], rmin[2];
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      float m = d2[0][nb][0];
+    for (int nb = 0; nb < kBlocks; ++nb) cmin[nb] = inf;
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+    for (int h = 0; h < 2; ++h) {
+      float rv[32];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) m = nmin(m, d2[mb][nb][v]);
-      cmin[nb] = m;
+      for (int m2 = 0; m2 < 2; ++m2) {
+        const int mb = 2 * h + m2;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int i0 = wr0 + mb * 32 + g * 8 + lh * 4;
+          const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[i0]);
+          const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[i0]);
+          const float rnv[4] = {rn.x, rn.y, rn.z, rn.w};
+          const float rs[4] = {ri.x, ri.y, ri.z, ri.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float m = inf;
+#pragma unroll
+            for (int nb = 0; nb < kBlocks; ++nb) {  // clamped at 0 by min_key, after the minima
+              const float d = fmaf(rs[e] * ci[nb], acc[mb][nb][g * 4 + e], rnv[e] + cn[nb]);
+              cmin[nb] = nmin(cmin[nb], d);
+              m = nmin(m, d);
+            }
+            rv[m2 * 16 + g * 4 + e] = m;
+          }
+        }
+      }
+      // row wr0 + h*64 + transposed_row(lr, lh): minimum over the wave's 128 columns
+      rmin[h] = transpose_min32(rv, lr);
     }
+    // column wc0 + (2q + lh)*32 + lr: minimum over the wave's 128 rows
     float cm[2];
 #pragma unroll
     for (int q = 0; q < 2; ++q) cm[q] = halves_min2(cmin[2 * q], cmin[2 * q + 1]);
-    // row minima over this wave's 128 columns: in-lane over nb, then the transposing
-    // butterfly over the 32 lanes of each half
-    float rv[32];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int v = 0; v < 16; ++v)
-        rv[mb * 16 + v] = nmin(nmin(d2[mb][0][v], d2[mb][1][v]), nmin(d2[mb][2][v], d2[mb][3][v]));
-    transpose_min32(rv, lr);
     __syncthreads();  // operand buffers are no longer read
-    float* s_cmin = reinterpret_cast<float*>(smem);  // [2 (wm)][TC]
-    float* s_rmin = s_cmin + 2 * TC;                  // [2 (wn)][TR]
+    float* s_cmin = reinterpret_cast<float*>(smem);  // [2 (wm)][TM]
+    float* s_rmin = s_cmin + 2 * TM;                  // [2 (wn)][TM]
 #pragma unroll
-    for (int q = 0; q < 2; ++q) s_cmin[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = cm[q];
-    s_rmin[wn * TR + wm * 64 + transposed_row(lr, lh)] = rv[0];
+    for (int q = 0; q < 2; ++q) s_cmin[wm * TM + wc0 + (2 * q + lh) * 32 + lr] = cm[q];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) s_rmin[wn * TM + wr0 + h * 64 + transposed_row(lr, lh)] = rmin[h];
     __syncthreads();
-    atomicMin(minbits + (long long)(col0 + t) * n + rA, min_key(nmin(s_cmin[t], s_cmin[TC + t])));
-    if (t < TR)
-      atomicMin(minbits + (long long)(row0 + t) * n + cA, min_key(nmin(s_rmin[t], s_rmin[TR + t])));
+    atomicMin(minbits + (long long)(col0 + t) * n + rA, min_key(nmin(s_cmin[t], s_cmin[TM + t])));
+    atomicMin(minbits + (long long)(row0 + t) * n + cA, min_key(nmin(s_rmin[t], s_rmin[TM + t])));
     return;
   }
 
@@ -368,138 +412,190 @@ __global__ __launch_bounds__(THREADS, 2) void split_pair_kernel(const _Float16* 
   // dimension).  Tile rows [0, rsplit) are image rA, the rest image rA + 1 or padding;
   // columns likewise with csplit and cA.  Whether a pair is masked (same image, or
   // padding) depends only on the two segments, so minima are taken per segment over
-  // the raw distances and a masked segment pair becomes +inf afterwards; a wave whose
-  // rows (or columns) lie in one segment reduces them without per-distance selects.
-  const int rsplit = min(TR, min((rA + 1) * p, rows) - row0);
-  const int csplit = min(TC, min((cA + 1) * p, rows) - col0);
+  // the raw distances and a masked segment pair becomes +inf afterwards.  The wave's
+  // 128 rows go as two 64-row halves; the accumulators of the second half wait in LDS
+  // (the ring is no longer read: 32 KB per wave, lane-contiguous 16-byte entries), so
+  // that the first half is reduced with half the accumulator registers free.
+  const int rsplit = min(TM, min((rA + 1) * p, rows) - row0);
+  const int csplit = min(TM, min((cA + 1) * p, rows) - col0);
   const int rBimg = row0 + rsplit < rows ? rA + 1 : n;  // used only when segment B is not empty
   const int cBimg = col0 + csplit < rows ? cA + 1 : n;
   const bool mAA = rA == cA, mAB = cBimg == n || rA == cBimg;
   const bool mBA = rBimg == n || rBimg == cA, mBB = rBimg == n || cBimg == n || rBimg == cBimg;
-  const int wr0 = wm * 64, wc0 = wn * 128;
-  float cminA[4], cminB[4];
-  if (rsplit >= wr0 + 64 || rsplit <= wr0) {
-    const bool inA = rsplit > wr0;
+  __syncthreads();  // every wave's last operand reads are done
+  constexpr int kStashBytes = NSTAGE * kStageBytes / (THREADS / kWave);
+  static_assert(kStashBytes >= 32 * kWave * 16, "stash: 32 entries of 16 bytes per lane");
+  float4* stash = reinterpret_cast<float4*>(smem + wave * kStashBytes);
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      float m = d2[0][nb][0];
+  for (int m2 = 0; m2 < 2; ++m2)
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+    for (int nb = 0; nb < kBlocks; ++nb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) m = nmin(m, d2[mb][nb][v]);
-      cminA[nb] = inA ? m : inf;
-      cminB[nb] = inA ? inf : m;
-    }
-  } else {
+      for (int g = 0; g < 4; ++g)
+        stash[((m2 * kBlocks + nb) * 4 + g) * kWave + lane] = make_float4(
+            acc[2 + m2][nb][g * 4], acc[2 + m2][nb][g * 4 + 1], acc[2 + m2][nb][g * 4 + 2], acc[2 + m2][nb][g * 4 + 3]);
+  float cmA[2] = {inf, inf}, cmB[2] = {inf, inf};  // per segment, over both halves (masked below)
+  float rmA[2], rmB[2];
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      float a = inf, b = inf;
+  for (int h = 0; h < 2; ++h) {
+    const int wr0 = wm * kWaveTile + h * 64;  // this half's 64 rows
+    float d2[2][kBlocks][16];
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+    for (int m2 = 0; m2 < 2; ++m2)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const bool inB = wr0 + mb * 32 + (v >> 2) * 8 + lh * 4 + (v & 3) >= rsplit;
-          a = nmin(a, inB ? inf : d2[mb][nb][v]);
-          b = nmin(b, inB ? d2[mb][nb][v] : inf);
+      for (int g = 0; g < 4; ++g) {
+        const int i0 = wr0 + m2 * 32 + g * 8 + lh * 4;
+        const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[i0]);
+        const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[i0]);
+        const float rnv[4] = {rn.x, rn.y, rn.z, rn.w};
+        const float rs[4] = {ri.x, ri.y, ri.z, ri.w};
+#pragma unroll
+        for (int nb = 0; nb < kBlocks; ++nb) {
+          float dot[4];
+          if (h == 0) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dot[e] = acc[m2][nb][g * 4 + e];
+          } else {
+            const float4 x = stash[((m2 * kBlocks + nb) * 4 + g) * kWave + lane];
+            dot[0] = x.x;
+            dot[1] = x.y;
+            dot[2] = x.z;
+            dot[3] = x.w;
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e)  // clamped at 0 by min_key, after the minima
+            d2[m2][nb][g * 4 + e] = fmaf(rs[e] * ci[nb], dot[e], rnv[e] + cn[nb]);
         }
-      cminA[nb] = a;
-      cminB[nb] = b;
+      }
+    // column minima over these 64 rows, per row segment
+    float cminA[kBlocks], cminB[kBlocks];
+    if (rsplit >= wr0 + 64 || rsplit <= wr0) {
+      const bool inA = rsplit > wr0;
+#pragma unroll
+      for (int nb = 0; nb < kBlocks; ++nb) {
+        float m = d2[0][nb][0];
+#pragma unroll
+        for (int m2 = 0; m2 < 2; ++m2)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) m = nmin(m, d2[m2][nb][v]);
+        cminA[nb] = inA ? m : inf;
+        cminB[nb] = inA ? inf : m;
+      }
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < kBlocks; ++nb) {
+        float a = inf, b = inf;
+#pragma unroll
+        for (int m2 = 0; m2 < 2; ++m2)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const bool inB = wr0 + m2 * 32 + (v >> 2) * 8 + lh * 4 + (v & 3) >= rsplit;
+            a = nmin(a, inB ? inf : d2[m2][nb][v]);
+            b = nmin(b, inB ? d2[m2][nb][v] : inf);
+          }
+        cminA[nb] = a;
+        cminB[nb] = b;
+      }
     }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {  // column wc0 + (2q + lh) * 32 + lr
+      cmA[q] = nmin(cmA[q], halves_min2(cminA[2 * q], cminA[2 * q + 1]));
+      cmB[q] = nmin(cmB[q], halves_min2(cminB[2 * q], cminB[2 * q + 1]));
+    }
+    // row minima over the wave's 128 columns, per column segment
+    float rowminA, rowminB;
+    if (csplit >= wc0 + kWaveTile || csplit <= wc0) {
+      float rv[32];
+#pragma unroll
+      for (int m2 = 0; m2 < 2; ++m2)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          rv[m2 * 16 + v] = nmin(nmin(d2[m2][0][v], d2[m2][1][v]), nmin(d2[m2][2][v], d2[m2][3][v]));
+      const float m = transpose_min32(rv, lr);
+      const bool inA = csplit > wc0;
+      rowminA = inA ? m : inf;
+      rowminB = inA ? inf : m;
+    } else {
+      bool colB[kBlocks];
+#pragma unroll
+      for (int nb = 0; nb < kBlocks; ++nb) colB[nb] = wc0 + nb * 32 + lr >= csplit;
+      {
+        float rv[32];
+#pragma unroll
+        for (int m2 = 0; m2 < 2; ++m2)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            float m = inf;
+#pragma unroll
+            for (int nb = 0; nb < kBlocks; ++nb) m = nmin(m, colB[nb] ? inf : d2[m2][nb][v]);
+            rv[m2 * 16 + v] = m;
+          }
+        rowminA = transpose_min32(rv, lr);
+      }
+      {
+        float rv[32];
+#pragma unroll
+        for (int m2 = 0; m2 < 2; ++m2)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            float m = inf;
+#pragma unroll
+            for (int nb = 0; nb < kBlocks; ++nb) m = nmin(m, colB[nb] ? d2[m2][nb][v] : inf);
+            rv[m2 * 16 + v] = m;
+          }
+        rowminB = transpose_min32(rv, lr);
+      }
+    }
+    const bool rowInB = wr0 + transposed_row(lr, lh) >= rsplit;
+    rmA[h] = (rowInB ? mBA : mAA) ? inf : rowminA;
+    rmB[h] = (rowInB ? mBB : mAB) ? inf : rowminB;
   }
-  float cmA[2], cmB[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    cmA[q] = halves_min2(cminA[2 * q], cminA[2 * q + 1]);  // column wc0 + (2q + lh) * 32 + lr
-    cmB[q] = halves_min2(cminB[2 * q], cminB[2 * q + 1]);
     const bool colInB = wc0 + (2 * q + lh) * 32 + lr >= csplit;
     if (colInB ? mAB : mAA) cmA[q] = inf;
     if (colInB ? mBB : mBA) cmB[q] = inf;
   }
-  float rowminA, rowminB;
-  if (csplit >= wc0 + 128 || csplit <= wc0) {
-    float rv[32];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int v = 0; v < 16; ++v)
-        rv[mb * 16 + v] = nmin(nmin(d2[mb][0][v], d2[mb][1][v]), nmin(d2[mb][2][v], d2[mb][3][v]));
-    const float m = transpose_min32(rv, lr);
-    const bool inA = csplit > wc0;
-    rowminA = inA ? m : inf;
-    rowminB = inA ? inf : m;
-  } else {
-    bool colB[4];
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) colB[nb] = wc0 + nb * 32 + lr >= csplit;
-    {
-      float rv[32];
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          float m = inf;
-#pragma unroll
-          for (int nb = 0; nb < 4; ++nb) m = nmin(m, colB[nb] ? inf : d2[mb][nb][v]);
-          rv[mb * 16 + v] = m;
-        }
-      rowminA = transpose_min32(rv, lr);
-    }
-    {
-      float rv[32];
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          float m = inf;
-#pragma unroll
-          for (int nb = 0; nb < 4; ++nb) m = nmin(m, colB[nb] ? d2[mb][nb][v] : inf);
-          rv[mb * 16 + v] = m;
-        }
-      rowminB = transpose_min32(rv, lr);
-    }
-  }
-  const int rk = wm * 64 + transposed_row(lr, lh);
-  {
-    const bool rowInB = rk >= rsplit;
-    if (rowInB ? mBA : mAA) rowminA = inf;
-    if (rowInB ? mBB : mAB) rowminB = inf;
-  }
-  __syncthreads();  // operand buffers are no longer read
-  float* s_cminA = reinterpret_cast<float*>(smem);  // [2 (wm)][TC]
-  float* s_cminB = s_cminA + 2 * TC;
-  float* s_rminA = s_cminB + 2 * TC;                 // [2 (wn)][TR]
-  float* s_rminB = s_rminA + 2 * TR;
+  __syncthreads();  // the stash is no longer read
+  float* s_cminA = reinterpret_cast<float*>(smem);  // [2 (wm)][TM]
+  float* s_cminB = s_cminA + 2 * TM;
+  float* s_rminA = s_cminB + 2 * TM;                 // [2 (wn)][TM]
+  float* s_rminB = s_rminA + 2 * TM;
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    s_cminA[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = cmA[q];
-    s_cminB[wm * TC + wn * 128 + (2 * q + lh) * 32 + lr] = cmB[q];
+    s_cminA[wm * TM + wc0 + (2 * q + lh) * 32 + lr] = cmA[q];
+    s_cminB[wm * TM + wc0 + (2 * q + lh) * 32 + lr] = cmB[q];
   }
-  s_rminA[wn * TR + rk] = rowminA;
-  s_rminB[wn * TR + rk] = rowminB;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int rk = wm * kWaveTile + h * 64 + transposed_row(lr, lh);
+    s_rminA[wn * TM + rk] = rmA[h];
+    s_rminB[wn * TM + rk] = rmB[h];
+  }
   __syncthreads();
   {
     const int cc = col0 + t;
     if (cc < rows) {
       // a segment with no pair of different images is exactly +inf (masked): skip it,
       // also because segment B may be the padding image n
-      const float a = nmin(s_cminA[t], s_cminA[TC + t]);
-      const float b = nmin(s_cminB[t], s_cminB[TC + t]);
+      const float a = nmin(s_cminA[t], s_cminA[TM + t]);
+      const float b = nmin(s_cminB[t], s_cminB[TM + t]);
       if (a != inf) atomicMin(minbits + (long long)cc * n + rA, min_key(a));
       if (b != inf) atomicMin(minbits + (long long)cc * n + rA + 1, min_key(b));
     }
   }
-  if (t < TR) {
+  {
     const int r = row0 + t;
     if (r < rows) {
-      const float a = nmin(s_rminA[t], s_rminA[TR + t]);
-      const float b = nmin(s_rminB[t], s_rminB[TR + t]);
+      const float a = nmin(s_rminA[t], s_rminA[TM + t]);
+      const float b = nmin(s_rminB[t], s_rminB[TM + t]);
       if (a != inf) atomicMin(minbits + (long long)r * n + cA, min_key(a));
       if (b != inf) atomicMin(minbits + (long long)r * n + cA + 1, min_key(b));
     }
   }
 }
 
-inline int nkb_of(int c) { return (c + KB - 1) / KB; }
+inline int nkb_of(int c) { return (c + 2 * KB - 1) / (2 * KB) * 2; }
 
 inline size_t split_array_bytes(long long rows, int c) { return align_up((size_t)rows * nkb_of(c) * ROWB, 256); }
 
@@ -516,7 +612,7 @@ inline int validate(int n, int p, int c, void* ws, size_t ws_bytes) {
   const long long rows = (long long)n * p;
   if (rows > (1LL << 30) || n > 4096) return MUSC_ERR_UNSUPPORTED;
   // 32-bit offsets within a 256-row panel (the buffer resources are based at each tile's panels)
-  if ((long long)TC * nkb_of(c) * ROWB > 0x7fffffffLL) return MUSC_ERR_UNSUPPORTED;
+  if ((long long)TM * nkb_of(c) * ROWB > 0x7fffffffLL) return MUSC_ERR_UNSUPPORTED;
   if (!ws || ws_bytes < workspace_bytes(n, p, c)) return MUSC_ERR_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0) return MUSC_ERR_INVALID_ARG;
   return MUSC_OK;
@@ -536,7 +632,7 @@ inline int run_pairs(int n, int p, int c, void* ws, hipStream_t s) {
   const long long rows = (long long)n * p;
   const long long T = (rows + TM - 1) / TM;
   const long long ntiles = total_tiles(T);
-  const long long grid = (2 * ntiles + kXcds - 1) / kXcds * kXcds;  // two half-tile workgroups per tile
+  const long long grid = (ntiles + kXcds - 1) / kXcds * kXcds;  // one workgroup per tile
   if (grid > 0x7fffffffLL) return MUSC_ERR_UNSUPPORTED;
   const Workspace w = carve(ws, n, p);
   hipLaunchKernelGGL(split_pair_kernel, dim3((unsigned)grid), dim3(THREADS), 0, s, split_array(ws, n, p), w.norms,

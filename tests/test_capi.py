@@ -72,11 +72,12 @@ def test_msm_split_workspace_and_argument_errors(lib):
     out, base = ctypes.c_size_t(), ctypes.c_size_t()
     assert lib.musc_msm_split_workspace_bytes(83, 1369, 1024, ctypes.byref(out)) == 0
     assert lib.musc_msm_workspace_bytes(83, 1369, 1024, ctypes.byref(base)) == 0
-    # the fp32 engine's workspace, then hi[16] | lo[16] fp16 (64 bytes) per row and 16-channel block
+    # the fp32 engine's workspace, then hi[16] | lo[16] fp16 (64 bytes) per row and 16-channel
+    # block, the blocks padded to an even count (the pair kernel takes two stages per iteration)
     assert out.value == base.value + align(83 * 1369 * (1024 // 16) * 64)
     assert lib.musc_msm_split_workspace_bytes(5, 300, 33, ctypes.byref(out)) == 0
     assert lib.musc_msm_workspace_bytes(5, 300, 33, ctypes.byref(base)) == 0
-    assert out.value == base.value + align(5 * 300 * 3 * 64)  # 33 channels -> 3 zero-padded blocks
+    assert out.value == base.value + align(5 * 300 * 4 * 64)  # 33 channels -> 4 zero-padded blocks
     assert lib.musc_msm_split_workspace_bytes(1, 300, 16, ctypes.byref(out)) == 1001
     fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
     big = ctypes.c_size_t(1 << 40)
