@@ -177,15 +177,7 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
   const bool simple = (row0 + TM <= rows) && (col0 + TM <= rows) && (rlast / p == rimg0) && (clast / p == cimg0);
   if (simple && rimg0 == cimg0) return;
 
-  const int t = threadIdx.x;  // THREADS == TM: thread t stages tile row t and tile column t
-  {
-    const int r = row0 + t, cc = col0 + t;
-    s_rnorm[t] = r < rows ? norms[r] : 0.f;
-    s_rinv[t] = r < rows ? -2.f * inv[r] : 0.f;  // -2 x row scale (exact)
-    s_cnorm[t] = cc < rows ? norms[cc] : 0.f;
-    s_cinv[t] = cc < rows ? inv[cc] : 0.f;
-  }
-
+  const int t = threadIdx.x;  // THREADS == TM: thread t merges tile row t and tile column t
   const int wave = t / kWave, lane = t % kWave;
   const int wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
@@ -307,6 +299,34 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
   // buffer into registers it never uses.  nkb is even (the split array is padded to
   // whole pairs of stages), so the loop takes two steps per iteration with the two
   // register sets in fixed roles.
+  // The norms and epilogue scales of the tile's rows and columns go into LDS the same way
+  // (lane l of a dword load lands at M0 + 4 l; wave wv takes entries wv*64 .. +63), issued
+  // before the stages' loads, so they have landed once stage 0 has (loads complete in
+  // order) and no wave waits for them at the start of the tile; entries past the pool's
+  // last row read 0 (the buffer extent).
+  {
+    auto vec_rsrc = [&](const float* base, int first) {
+      const unsigned long long addr = reinterpret_cast<unsigned long long>(base + first);
+      int4v r;
+      r.x = (int)(uint32_t)(addr & 0xffffffffull);
+      r.y = (int)(uint32_t)(addr >> 32);
+      r.z = min(rows - first, TM) * 4;
+      r.w = kBufferFlags;
+      return r;
+    };
+    const uint32_t nvoff = (uint32_t)((wave * kWave + lane) * 4);
+    auto load_vec = [&](const int4v& rs, float* dst) {
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(lds_void*)dst + (uint32_t)(wv * kWave * 4));
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                   :
+                   : "s"(m0), "v"(nvoff), "s"(rs)
+                   : "memory", "m0");
+    };
+    load_vec(vec_rsrc(norms, row0), s_rnorm);
+    load_vec(vec_rsrc(inv, row0), s_rinv);
+    load_vec(vec_rsrc(norms, col0), s_cnorm);
+    load_vec(vec_rsrc(inv, col0), s_cinv);
+  }
   for (int st = 0; st < NSTAGE && st < nkb; ++st) issue(st, st);
   wait_stage(0, min(NSTAGE, nkb) - 1);
   __syncthreads();
@@ -374,7 +394,7 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
           const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[i0]);
           const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[i0]);
           const float rnv[4] = {rn.x, rn.y, rn.z, rn.w};
-          const float rs[4] = {ri.x, ri.y, ri.z, ri.w};
+          const float rs[4] = {-2.f * ri.x, -2.f * ri.y, -2.f * ri.z, -2.f * ri.w};  // -2 x row scale (exact)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             float m = inf;
@@ -448,7 +468,7 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
         const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[i0]);
         const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[i0]);
         const float rnv[4] = {rn.x, rn.y, rn.z, rn.w};
-        const float rs[4] = {ri.x, ri.y, ri.z, ri.w};
+        const float rs[4] = {-2.f * ri.x, -2.f * ri.y, -2.f * ri.z, -2.f * ri.w};  // -2 x row scale (exact)
 #pragma unroll
         for (int nb = 0; nb < kBlocks; ++nb) {
           float dot[4];
