@@ -94,6 +94,27 @@ def test_minima_vs_f64_bruteforce(device):
     np.testing.assert_allclose(got[fin], ref[fin], rtol=0, atol=2e-6)
 
 
+# Image boundaries at many offsets inside the 256 x 256 tiles: a pool of n images of p
+# rows puts boundaries at k p (k = 1 .. n-1), i.e. at offsets k p mod 256 within a tile.
+# p = 264 gives offsets on 8-row group edges; 261 and 269 offsets inside groups, in both
+# lane halves (rows lh*4 + e); 383 and 385 offsets next to the 128-row wave edge and the
+# 64-row half edge; 300 and 449 mixed.  The straddling tiles are reduced per image segment
+# in 64-row halves; every per-(row, image) minimum is checked, so a distance credited to
+# the wrong segment shows.
+@pytest.mark.parametrize('p', [261, 264, 269, 300, 383, 385, 449])
+def test_minima_at_boundary_offsets_vs_f64_bruteforce(device, p):
+    n = 8
+    torch.manual_seed(p)
+    z = torch.nn.functional.normalize(torch.randn((n, p, 48)) + 0.3 * torch.randn((1, 1, 48)), dim=-1)
+    offs = sorted({(k * p) % 256 for k in range(1, n)})
+    got = _split_minima(z.to(device), normalize=False)
+    ref = oracle.msm_nearest_f64_c(z.numpy()) ** 2
+    fin = np.isfinite(ref)
+    print(f'p={p}: boundary offsets {offs}', flush=True)
+    assert np.isinf(got[~fin]).all(), 'own-image entries must stay +inf'
+    np.testing.assert_allclose(got[fin], ref[fin], rtol=0, atol=2e-6)
+
+
 def test_config1_plumbing_kernel_level(device):
     z = synthetic.msm_features(8, 1369, 1024, seed=42)
     zd = z.to(device)
