@@ -10,23 +10,25 @@ from musc_hip import _attention_hip, _epilogue_hip, pipeline
 pytestmark = pytest.mark.gpu
 
 
-def _work(tokens, q, k, v):
+def _work(tokens, q, k, v, engine='fp32'):
     pools = pipeline.lnamd_pools(tokens, [1, 3])
-    scores = pipeline.msm_all(pools)
+    scores = pipeline.msm_all(pools, engine=engine)
     maps, img = _epilogue_hip.maps_and_scores(scores, 40)
     att = _attention_hip.attention(q, k, v, 0.125)
     return maps, img, att
 
 
-def _inputs(seed, device):
+def _inputs(seed, device, side=7):
     g = torch.Generator().manual_seed(seed)
-    tokens = [torch.randn((6, 1 + 7 * 7, 48), generator=g).to(device) for _ in range(2)]
+    tokens = [torch.randn((6, 1 + side * side, 48), generator=g).to(device) for _ in range(2)]
     q, k, v = (torch.randn((4, 300, 64), generator=g).to(device) for _ in range(3))
     return tokens, q, k, v
 
 
-def test_threads_on_separate_streams_match_sequential(device):
-    inputs = [_inputs(s, device) for s in (11, 12)]
+# the split engine needs P >= 256: 17 x 17 grids (P = 289, tiles straddling image boundaries)
+@pytest.mark.parametrize('engine,side', [('fp32', 7), ('split16', 17)])
+def test_threads_on_separate_streams_match_sequential(device, engine, side):
+    inputs = [_inputs(s, device, side) + (engine,) for s in (11, 12)]
     expected = [_work(*x) for x in inputs]
     torch.cuda.synchronize()
     results = [[None] * 8, [None] * 8]
