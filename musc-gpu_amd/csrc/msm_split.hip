@@ -382,34 +382,74 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
     float cmin[kBlocks], rmin[2];
 #pragma unroll
     for (int nb = 0; nb < kBlocks; ++nb) cmin[nb] = inf;
+    // Unit rows: when every row and column of this wave has norm 1 and scale 2^-10 (rows
+    // L2-normalised by the prepare stage), each distance is fma(-2^-19, dot, 2) -- the
+    // general formula with those values, exactly -- which never increases with the dot,
+    // and rounding keeps that order: the minimum distance over any set of pairs is
+    // fma(-2^-19, maximum dot, 2), bit for bit (NaN and infinities included).  Then only
+    // the dots are reduced (as minima of their negations, with the same butterflies) and
+    // the formula is applied to the four minima of each lane.
+    const float kUnit = 1.f / (float)(1 << kScaleShift);
+    bool unit = true;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      float rv[32];
+    for (int k = 0; k < 2; ++k) {
+      const int rr = wr0 + k * 64 + lane, cc2 = wc0 + k * 64 + lane;
+      unit = unit && s_rnorm[rr] == 1.f && s_rinv[rr] == kUnit && s_cnorm[cc2] == 1.f && s_cinv[cc2] == kUnit;
+    }
+    if (__all(unit)) {
+      constexpr float kNegUnitScale = 2.f / (float)(1 << (2 * kScaleShift));  // -(-2 x 2^-10 x 2^-10)
 #pragma unroll
-      for (int m2 = 0; m2 < 2; ++m2) {
-        const int mb = 2 * h + m2;
+      for (int h = 0; h < 2; ++h) {
+        float rv[32];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int i0 = wr0 + mb * 32 + g * 8 + lh * 4;
-          const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[i0]);
-          const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[i0]);
-          const float rnv[4] = {rn.x, rn.y, rn.z, rn.w};
-          const float rs[4] = {-2.f * ri.x, -2.f * ri.y, -2.f * ri.z, -2.f * ri.w};  // -2 x row scale (exact)
+        for (int m2 = 0; m2 < 2; ++m2) {
+          const int mb = 2 * h + m2;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
+          for (int v = 0; v < 16; ++v) {
             float m = inf;
 #pragma unroll
-            for (int nb = 0; nb < kBlocks; ++nb) {  // clamped at 0 by min_key, after the minima
-              const float d = fmaf(rs[e] * ci[nb], acc[mb][nb][g * 4 + e], rnv[e] + cn[nb]);
-              cmin[nb] = nmin(cmin[nb], d);
-              m = nmin(m, d);
+            for (int nb = 0; nb < kBlocks; ++nb) {
+              const float x = -acc[mb][nb][v];
+              cmin[nb] = nmin(cmin[nb], x);
+              m = nmin(m, x);
             }
-            rv[m2 * 16 + g * 4 + e] = m;
+            rv[m2 * 16 + v] = m;
           }
         }
+        rmin[h] = fmaf(kNegUnitScale, transpose_min32(rv, lr), 2.f);
       }
-      // row wr0 + h*64 + transposed_row(lr, lh): minimum over the wave's 128 columns
-      rmin[h] = transpose_min32(rv, lr);
+#pragma unroll
+      for (int nb = 0; nb < kBlocks; ++nb) cmin[nb] = fmaf(kNegUnitScale, cmin[nb], 2.f);
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float rv[32];
+#pragma unroll
+        for (int m2 = 0; m2 < 2; ++m2) {
+          const int mb = 2 * h + m2;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int i0 = wr0 + mb * 32 + g * 8 + lh * 4;
+            const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[i0]);
+            const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[i0]);
+            const float rnv[4] = {rn.x, rn.y, rn.z, rn.w};
+            const float rs[4] = {-2.f * ri.x, -2.f * ri.y, -2.f * ri.z, -2.f * ri.w};  // -2 x row scale (exact)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float m = inf;
+#pragma unroll
+              for (int nb = 0; nb < kBlocks; ++nb) {  // clamped at 0 by min_key, after the minima
+                const float d = fmaf(rs[e] * ci[nb], acc[mb][nb][g * 4 + e], rnv[e] + cn[nb]);
+                cmin[nb] = nmin(cmin[nb], d);
+                m = nmin(m, d);
+              }
+              rv[m2 * 16 + g * 4 + e] = m;
+            }
+          }
+        }
+        // row wr0 + h*64 + transposed_row(lr, lh): minimum over the wave's 128 columns
+        rmin[h] = transpose_min32(rv, lr);
+      }
     }
     // column wc0 + (2q + lh)*32 + lr: minimum over the wave's 128 rows
     float cm[2];
@@ -456,37 +496,67 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
             acc[2 + m2][nb][g * 4], acc[2 + m2][nb][g * 4 + 1], acc[2 + m2][nb][g * 4 + 2], acc[2 + m2][nb][g * 4 + 3]);
   float cmA[2] = {inf, inf}, cmB[2] = {inf, inf};  // per segment, over both halves (masked below)
   float rmA[2], rmB[2];
+  // unit rows and columns (see the one-image-pair case): reduce the negated dots and
+  // apply fma(2^-19, ., 2) to the eight results; a masked +inf stays +inf
+  const float kUnit = 1.f / (float)(1 << kScaleShift);
+  constexpr float kNegUnitScale = 2.f / (float)(1 << (2 * kScaleShift));
+  bool unit = true;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int rr = wm * kWaveTile + k * 64 + lane, cc2 = wc0 + k * 64 + lane;
+    unit = unit && s_rnorm[rr] == 1.f && s_rinv[rr] == kUnit && s_cnorm[cc2] == 1.f && s_cinv[cc2] == kUnit;
+  }
+  const bool unitw = __all(unit);
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int wr0 = wm * kWaveTile + h * 64;  // this half's 64 rows
     float d2[2][kBlocks][16];
+    auto fill = [&](auto unit_c) {
 #pragma unroll
-    for (int m2 = 0; m2 < 2; ++m2)
+      for (int m2 = 0; m2 < 2; ++m2)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int i0 = wr0 + m2 * 32 + g * 8 + lh * 4;
-        const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[i0]);
-        const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[i0]);
-        const float rnv[4] = {rn.x, rn.y, rn.z, rn.w};
-        const float rs[4] = {-2.f * ri.x, -2.f * ri.y, -2.f * ri.z, -2.f * ri.w};  // -2 x row scale (exact)
-#pragma unroll
-        for (int nb = 0; nb < kBlocks; ++nb) {
-          float dot[4];
-          if (h == 0) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) dot[e] = acc[m2][nb][g * 4 + e];
-          } else {
-            const float4 x = stash[((m2 * kBlocks + nb) * 4 + g) * kWave + lane];
-            dot[0] = x.x;
-            dot[1] = x.y;
-            dot[2] = x.z;
-            dot[3] = x.w;
+        for (int g = 0; g < 4; ++g) {
+          float rnv[4] = {0.f, 0.f, 0.f, 0.f}, rs[4] = {0.f, 0.f, 0.f, 0.f};
+          if constexpr (!decltype(unit_c)::value) {
+            const int i0 = wr0 + m2 * 32 + g * 8 + lh * 4;
+            const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[i0]);
+            const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[i0]);
+            rnv[0] = rn.x;
+            rnv[1] = rn.y;
+            rnv[2] = rn.z;
+            rnv[3] = rn.w;
+            rs[0] = -2.f * ri.x;  // -2 x row scale (exact)
+            rs[1] = -2.f * ri.y;
+            rs[2] = -2.f * ri.z;
+            rs[3] = -2.f * ri.w;
           }
 #pragma unroll
-          for (int e = 0; e < 4; ++e)  // clamped at 0 by min_key, after the minima
-            d2[m2][nb][g * 4 + e] = fmaf(rs[e] * ci[nb], dot[e], rnv[e] + cn[nb]);
+          for (int nb = 0; nb < kBlocks; ++nb) {
+            float dot[4];
+            if (h == 0) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) dot[e] = acc[m2][nb][g * 4 + e];
+            } else {
+              const float4 x = stash[((m2 * kBlocks + nb) * 4 + g) * kWave + lane];
+              dot[0] = x.x;
+              dot[1] = x.y;
+              dot[2] = x.z;
+              dot[3] = x.w;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {  // clamped at 0 by min_key, after the minima
+              if constexpr (decltype(unit_c)::value)
+                d2[m2][nb][g * 4 + e] = -dot[e];
+              else
+                d2[m2][nb][g * 4 + e] = fmaf(rs[e] * ci[nb], dot[e], rnv[e] + cn[nb]);
+            }
+          }
         }
-      }
+    };
+    if (unitw)
+      fill(std::true_type{});
+    else
+      fill(std::false_type{});
     // column minima over these 64 rows, per row segment
     float cminA[kBlocks], cminB[kBlocks];
     if (rsplit >= wr0 + 64 || rsplit <= wr0) {
@@ -569,6 +639,17 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
     const bool rowInB = wr0 + transposed_row(lr, lh) >= rsplit;
     rmA[h] = (rowInB ? mBA : mAA) ? inf : rowminA;
     rmB[h] = (rowInB ? mBB : mAB) ? inf : rowminB;
+    if (unitw) {
+      rmA[h] = fmaf(kNegUnitScale, rmA[h], 2.f);
+      rmB[h] = fmaf(kNegUnitScale, rmB[h], 2.f);
+    }
+  }
+  if (unitw) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      cmA[q] = fmaf(kNegUnitScale, cmA[q], 2.f);
+      cmB[q] = fmaf(kNegUnitScale, cmB[q], 2.f);
+    }
   }
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
