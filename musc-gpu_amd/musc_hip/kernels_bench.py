@@ -1,6 +1,7 @@
 """Per-kernel micro-benchmarks of libmusc_hip on one GPU (used for rocprofv3 runs).
 
     python musc-gpu_amd/musc_hip/kernels_bench.py msm [--n 83 --p 1369 --c 1024 --iters 3 --engine fp32|split16]
+                                                       [--normalize]
     python musc-gpu_amd/musc_hip/kernels_bench.py lnamd [--n 83 --layers 4 --iters 3]
     python musc-gpu_amd/musc_hip/kernels_bench.py attention [--dtype fp32|fp16 --blocks 24]
     python musc-gpu_amd/musc_hip/kernels_bench.py copy [--mib 1024 --iters 3]
@@ -55,14 +56,18 @@ def bench_msm(args):
     scores = torch.empty((n, p), dtype=torch.float64, device=dev)
     lib, s = rt.library(), rt.stream(dev)
     t = {'prepare': [], 'pairs': [], 'refine': [], 'rank': []}
+    # --normalize: rows scored as Z[i, q] / ||Z[i, q]|| inside the kernels, as the pipeline
+    # scores every LNAMD pool (models/musc.py:238)
+    flags = rt.MSM_NORMALIZE_ROWS if args.normalize else 0
     for it in range(args.iters + 1):
         evs = [_events() for _ in range(4)]
         evs[0][0].record()
         if engine == 'split16':
-            rt.check(lib.musc_msm_split_prepare_f32(z.data_ptr(), n, p, c, 0, ws.data_ptr(), ws.numel(), s),
+            rt.check(lib.musc_msm_split_prepare_f32(z.data_ptr(), n, p, c, flags, ws.data_ptr(), ws.numel(), s),
                      'prepare')
         else:
-            rt.check(lib.musc_msm_prepare_f32(z.data_ptr(), n, p, c, 0, ws.data_ptr(), ws.numel(), s), 'prepare')
+            rt.check(lib.musc_msm_prepare_f32(z.data_ptr(), n, p, c, flags, ws.data_ptr(), ws.numel(), s),
+                     'prepare')
         evs[0][1].record()
         evs[1][0].record()
         if engine == 'split16':
@@ -84,8 +89,8 @@ def bench_msm(args):
     avg = {k: sum(v) / len(v) for k, v in t.items()}
     flop = float(c) * p * p * n * (n - 1)
     tf = flop / (avg['pairs'] / 1e3) / 1e12
-    res = {'kernel': 'msm', 'engine': engine, 'n': n, 'p': p, 'c': c, 'avg_ms': avg, 'pair_flop': flop,
-           'pair_tflops': tf}
+    res = {'kernel': 'msm', 'engine': engine, 'n': n, 'p': p, 'c': c, 'normalize_rows': bool(args.normalize),
+           'avg_ms': avg, 'pair_flop': flop, 'pair_tflops': tf}
     if engine == 'split16':
         # three fp16 MFMA products per fp32 dot product: the fp16 matrix-core work is 3x the
         # algorithmic FLOP; tf is the fp32-equivalent rate
@@ -476,6 +481,7 @@ def main():
     ap.add_argument('--mib', type=int, default=1024)
     ap.add_argument('--iters', type=int, default=3)
     ap.add_argument('--engine', choices=['fp32', 'split16'], default='fp32', help='MSM dot-product engine')
+    ap.add_argument('--normalize', action='store_true', help='msm: normalise rows in the kernels (the pipeline\'s use)')
     ap.add_argument('--src', type=int, default=1024, help='preprocess: source image side')
     ap.add_argument('--workers', type=int, default=4, help='preprocess: host threads (the reference loader uses 4)')
     ap.add_argument('--files', type=int, default=0, help='preprocess: also time the loaders over this many PNG files')
