@@ -290,15 +290,6 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
   using F = std::false_type;
   using Tr = std::true_type;
 
-  // Stage j lives in LDS buffer j % NSTAGE.  Step j: wait for this thread's loads of
-  // stage j + 1; the barrier then makes every wave's loads of stage j + 1 visible and
-  // guarantees that every wave has finished reading stage j (its reads completed before
-  // the barrier; its operands are in registers), so buffer j % NSTAGE takes the loads of
-  // stage j + NSTAGE; then the MFMAs of stage j run from registers while the operands of
-  // stage j + 1 are read into the other register set.  The last step reads a stale
-  // buffer into registers it never uses.  nkb is even (the split array is padded to
-  // whole pairs of stages), so the loop takes two steps per iteration with the two
-  // register sets in fixed roles.
   // The norms and epilogue scales of the tile's rows and columns go into LDS the same way
   // (lane l of a dword load lands at M0 + 4 l; wave wv takes entries wv*64 .. +63), issued
   // before the stages' loads, so they have landed once stage 0 has (loads complete in
@@ -327,6 +318,15 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
     load_vec(vec_rsrc(norms, col0), s_cnorm);
     load_vec(vec_rsrc(inv, col0), s_cinv);
   }
+  // Stage j lives in LDS buffer j % NSTAGE.  Step j: wait for this thread's loads of
+  // stage j + 1; the barrier then makes every wave's loads of stage j + 1 visible and
+  // guarantees that every wave has finished reading stage j (its reads completed before
+  // the barrier; its operands are in registers), so buffer j % NSTAGE takes the loads of
+  // stage j + NSTAGE; then the MFMAs of stage j run from registers while the operands of
+  // stage j + 1 are read into the other register set.  The last step reads a stale
+  // buffer into registers it never uses.  nkb is even (the split array is padded to
+  // whole pairs of stages), so the loop takes two steps per iteration with the two
+  // register sets in fixed roles.
   for (int st = 0; st < NSTAGE && st < nkb; ++st) issue(st, st);
   wait_stage(0, min(NSTAGE, nkb) - 1);
   __syncthreads();
