@@ -34,18 +34,22 @@ def _raw_pool(seed, n=10, p=256, c=64):
     return torch.randn((n, p, c), generator=g) * 2.0 + 0.3
 
 
+# p = 256: tiles aligned with the images; p = 300: tiles straddling image boundaries.  With
+# the split engine, waves whose rows and columns all have unit norm reduce the dots alone,
+# the others (here those holding a NaN-norm row) the distances: both kinds in one pool.
+@pytest.mark.parametrize('p', [256, 300])
 @pytest.mark.parametrize('engine', ENGINES)
-def test_zero_and_nan_rows_with_row_normalisation(device, engine):
+def test_zero_and_nan_rows_with_row_normalisation(device, engine, p):
     # rows scored as z / ||z|| (MUSC_MSM_NORMALIZE_ROWS): a zero row is 0/0 = NaN as in
     # musc.py:238, a row holding a NaN is NaN, a zero image is all NaN
-    z = _raw_pool(1)
+    z = _raw_pool(1, p=p)
     z[2, 5, 7] = float('nan')
     z[4, 9] = 0.0
     z[6] = 0.0
     got = _MSM_hip.MSM(z.to(device), normalize_rows=True, engine=engine).cpu()
     ref = om.MSM(z / z.norm(dim=-1, keepdim=True))
     res = _check(ref.numpy(), got.numpy(), f'{engine} normalised rows')
-    assert res['reference_nan'] == 2 + 256            # rows (2, 5), (4, 9) and image 6
+    assert res['reference_nan'] == 2 + p              # rows (2, 5), (4, 9) and image 6
     # the other images' scores are finite: the NaN minima rank last, outside [0, 2)
     assert torch.isfinite(got[[0, 1, 3, 5, 7, 8, 9]]).all()
 
