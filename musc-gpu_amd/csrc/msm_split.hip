@@ -364,6 +364,17 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
   // Epilogue.  Lane (lr, lh) of wave (wm, wn) holds, for mb, nb < 4, v < 16, the dot
   // of tile row wm*128 + mb*32 + (v/4)*8 + lh*4 + v%4 with tile column
   // wn*128 + nb*32 + lr.
+  // The thread's indices are derived again from an opaque copy of the thread index
+  // (the wave's in scalar registers): otherwise the compiler keeps their prologue
+  // values live across the main loop, where every register is taken, and spills them
+  // to scratch memory, whose reloads here each wait a full memory round trip.
+  int t_epi = threadIdx.x;
+  asm volatile("" : "+v"(t_epi));
+  {
+  const int t = t_epi;
+  const int wave = __builtin_amdgcn_readfirstlane(t_epi / kWave), lane = t_epi % kWave;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lr = lane & 31, lh = lane >> 5;
   const int rA = rimg0, cA = cimg0;
   const int wc0 = wn * kWaveTile;
   const float inf = __int_as_float(kInfBits);
@@ -472,32 +483,25 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
   // dimension).  Tile rows [0, rsplit) are image rA, the rest image rA + 1 or padding;
   // columns likewise with csplit and cA.  Whether a pair is masked (same image, or
   // padding) depends only on the two segments, so minima are taken per segment over
-  // the raw distances and a masked segment pair becomes +inf afterwards.  The wave's
-  // 128 rows go as two 64-row halves; the accumulators of the second half wait in LDS
-  // (the ring is no longer read: 32 KB per wave, lane-contiguous 16-byte entries), so
-  // that the first half is reduced with half the accumulator registers free.
+  // the raw distances and a masked segment pair becomes +inf afterwards.  Each 64-row
+  // half of the wave is reduced in one pass over its accumulators, as in the one-pair
+  // case: only a half that the row boundary crosses sorts each distance into the
+  // column minima of its row's segment, and only a wave that the column boundary
+  // crosses sorts it into the row minima of its column's segment (a select per
+  // distance, so that a NaN distance of a masked pair cannot reach an unmasked minimum).
   const int rsplit = min(TM, min((rA + 1) * p, rows) - row0);
   const int csplit = min(TM, min((cA + 1) * p, rows) - col0);
   const int rBimg = row0 + rsplit < rows ? rA + 1 : n;  // used only when segment B is not empty
   const int cBimg = col0 + csplit < rows ? cA + 1 : n;
   const bool mAA = rA == cA, mAB = cBimg == n || rA == cBimg;
   const bool mBA = rBimg == n || rBimg == cA, mBB = rBimg == n || cBimg == n || rBimg == cBimg;
-  __syncthreads();  // every wave's last operand reads are done
-  constexpr int kStashBytes = NSTAGE * kStageBytes / (THREADS / kWave);
-  static_assert(kStashBytes >= 32 * kWave * 16, "stash: 32 entries of 16 bytes per lane");
-  float4* stash = reinterpret_cast<float4*>(smem + wave * kStashBytes);
+  const bool colsplit = csplit > wc0 && csplit < wc0 + kWaveTile;  // the column boundary crosses this wave
+  const bool colsA = csplit >= wc0 + kWaveTile;                    // otherwise: all its columns in segment A
+  bool colB[kBlocks];
 #pragma unroll
-  for (int m2 = 0; m2 < 2; ++m2)
-#pragma unroll
-    for (int nb = 0; nb < kBlocks; ++nb)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        stash[((m2 * kBlocks + nb) * 4 + g) * kWave + lane] = make_float4(
-            acc[2 + m2][nb][g * 4], acc[2 + m2][nb][g * 4 + 1], acc[2 + m2][nb][g * 4 + 2], acc[2 + m2][nb][g * 4 + 3]);
-  float cmA[2] = {inf, inf}, cmB[2] = {inf, inf};  // per segment, over both halves (masked below)
-  float rmA[2], rmB[2];
+  for (int nb = 0; nb < kBlocks; ++nb) colB[nb] = wc0 + nb * 32 + lr >= csplit;
   // unit rows and columns (see the one-image-pair case): reduce the negated dots and
-  // apply fma(2^-19, ., 2) to the eight results; a masked +inf stays +inf
+  // apply fma(2^-19, ., 2) to the results; a masked +inf stays +inf
   const float kUnit = 1.f / (float)(1 << kScaleShift);
   constexpr float kNegUnitScale = 2.f / (float)(1 << (2 * kScaleShift));
   bool unit = true;
@@ -507,142 +511,121 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
     unit = unit && s_rnorm[rr] == 1.f && s_rinv[rr] == kUnit && s_cnorm[cc2] == 1.f && s_cinv[cc2] == kUnit;
   }
   const bool unitw = __all(unit);
+  float cminA[kBlocks], cminB[kBlocks];  // column minima per row segment, over both halves (masked below)
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int nb = 0; nb < kBlocks; ++nb) cminA[nb] = cminB[nb] = inf;
+  float rmA[2], rmB[2];
+  auto reduce_half = [&](auto h_c, auto unit_c, auto rowsplit_c, auto colsplit_c) {
+    constexpr int h = decltype(h_c)::value;
+    constexpr bool kUnitRows = decltype(unit_c)::value;
+    constexpr bool kRowSplit = decltype(rowsplit_c)::value, kColSplit = decltype(colsplit_c)::value;
     const int wr0 = wm * kWaveTile + h * 64;  // this half's 64 rows
-    float d2[2][kBlocks][16];
-    auto fill = [&](auto unit_c) {
+    float hA[kBlocks], hB[kBlocks];            // this half's column minima (per row segment when split)
 #pragma unroll
-      for (int m2 = 0; m2 < 2; ++m2)
+    for (int nb = 0; nb < kBlocks; ++nb) hA[nb] = hB[nb] = inf;
+    float rv[32], rvB[32];  // per row item: minimum over the columns (of segment A, B when split)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          float rnv[4] = {0.f, 0.f, 0.f, 0.f}, rs[4] = {0.f, 0.f, 0.f, 0.f};
-          if constexpr (!decltype(unit_c)::value) {
-            const int i0 = wr0 + m2 * 32 + g * 8 + lh * 4;
-            const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[i0]);
-            const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[i0]);
-            rnv[0] = rn.x;
-            rnv[1] = rn.y;
-            rnv[2] = rn.z;
-            rnv[3] = rn.w;
-            rs[0] = -2.f * ri.x;  // -2 x row scale (exact)
-            rs[1] = -2.f * ri.y;
-            rs[2] = -2.f * ri.z;
-            rs[3] = -2.f * ri.w;
-          }
+    for (int m2 = 0; m2 < 2; ++m2) {
+      const int mb = 2 * h + m2;
 #pragma unroll
-          for (int nb = 0; nb < kBlocks; ++nb) {
-            float dot[4];
-            if (h == 0) {
-#pragma unroll
-              for (int e = 0; e < 4; ++e) dot[e] = acc[m2][nb][g * 4 + e];
-            } else {
-              const float4 x = stash[((m2 * kBlocks + nb) * 4 + g) * kWave + lane];
-              dot[0] = x.x;
-              dot[1] = x.y;
-              dot[2] = x.z;
-              dot[3] = x.w;
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {  // clamped at 0 by min_key, after the minima
-              if constexpr (decltype(unit_c)::value)
-                d2[m2][nb][g * 4 + e] = -dot[e];
-              else
-                d2[m2][nb][g * 4 + e] = fmaf(rs[e] * ci[nb], dot[e], rnv[e] + cn[nb]);
-            }
-          }
+      for (int g = 0; g < 4; ++g) {
+        float rnv[4] = {0.f, 0.f, 0.f, 0.f}, rs[4] = {0.f, 0.f, 0.f, 0.f};
+        const int i0 = wr0 + m2 * 32 + g * 8 + lh * 4;
+        if constexpr (!kUnitRows) {
+          const float4 rn = *reinterpret_cast<const float4*>(&s_rnorm[i0]);
+          const float4 ri = *reinterpret_cast<const float4*>(&s_rinv[i0]);
+          rnv[0] = rn.x;
+          rnv[1] = rn.y;
+          rnv[2] = rn.z;
+          rnv[3] = rn.w;
+          rs[0] = -2.f * ri.x;  // -2 x row scale (exact)
+          rs[1] = -2.f * ri.y;
+          rs[2] = -2.f * ri.z;
+          rs[3] = -2.f * ri.w;
         }
-    };
-    if (unitw)
-      fill(std::true_type{});
-    else
-      fill(std::false_type{});
-    // column minima over these 64 rows, per row segment
-    float cminA[kBlocks], cminB[kBlocks];
-    if (rsplit >= wr0 + 64 || rsplit <= wr0) {
-      const bool inA = rsplit > wr0;
 #pragma unroll
-      for (int nb = 0; nb < kBlocks; ++nb) {
-        float m = d2[0][nb][0];
+        for (int e = 0; e < 4; ++e) {
+          const bool inB = i0 + e >= rsplit;
+          float mA = inf, mB = inf;
 #pragma unroll
-        for (int m2 = 0; m2 < 2; ++m2)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) m = nmin(m, d2[m2][nb][v]);
-        cminA[nb] = inA ? m : inf;
-        cminB[nb] = inA ? inf : m;
-      }
-    } else {
-#pragma unroll
-      for (int nb = 0; nb < kBlocks; ++nb) {
-        float a = inf, b = inf;
-#pragma unroll
-        for (int m2 = 0; m2 < 2; ++m2)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const bool inB = wr0 + m2 * 32 + (v >> 2) * 8 + lh * 4 + (v & 3) >= rsplit;
-            a = nmin(a, inB ? inf : d2[m2][nb][v]);
-            b = nmin(b, inB ? d2[m2][nb][v] : inf);
+          for (int nb = 0; nb < kBlocks; ++nb) {  // clamped at 0 by min_key, after the minima
+            const float dot = acc[mb][nb][g * 4 + e];
+            const float x = kUnitRows ? -dot : fmaf(rs[e] * ci[nb], dot, rnv[e] + cn[nb]);
+            if constexpr (kRowSplit) {
+              hA[nb] = nmin(hA[nb], inB ? inf : x);
+              hB[nb] = nmin(hB[nb], inB ? x : inf);
+            } else {
+              hA[nb] = nmin(hA[nb], x);
+            }
+            if constexpr (kColSplit) {
+              mA = nmin(mA, colB[nb] ? inf : x);
+              mB = nmin(mB, colB[nb] ? x : inf);
+            } else {
+              mA = nmin(mA, x);
+            }
           }
-        cminA[nb] = a;
-        cminB[nb] = b;
+          rv[m2 * 16 + g * 4 + e] = mA;
+          rvB[m2 * 16 + g * 4 + e] = mB;
+        }
       }
     }
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {  // column wc0 + (2q + lh) * 32 + lr
-      cmA[q] = nmin(cmA[q], halves_min2(cminA[2 * q], cminA[2 * q + 1]));
-      cmB[q] = nmin(cmB[q], halves_min2(cminB[2 * q], cminB[2 * q + 1]));
-    }
-    // row minima over the wave's 128 columns, per column segment
+    // row wr0 + transposed_row(lr, lh): minima over the wave's 128 columns, per column segment
     float rowminA, rowminB;
-    if (csplit >= wc0 + kWaveTile || csplit <= wc0) {
-      float rv[32];
-#pragma unroll
-      for (int m2 = 0; m2 < 2; ++m2)
-#pragma unroll
-        for (int v = 0; v < 16; ++v)
-          rv[m2 * 16 + v] = nmin(nmin(d2[m2][0][v], d2[m2][1][v]), nmin(d2[m2][2][v], d2[m2][3][v]));
-      const float m = transpose_min32(rv, lr);
-      const bool inA = csplit > wc0;
-      rowminA = inA ? m : inf;
-      rowminB = inA ? inf : m;
+    if constexpr (kColSplit) {
+      rowminA = transpose_min32(rv, lr);
+      rowminB = transpose_min32(rvB, lr);
     } else {
-      bool colB[kBlocks];
+      const float m = transpose_min32(rv, lr);
+      rowminA = colsA ? m : inf;
+      rowminB = colsA ? inf : m;
+    }
+    // this half's column minima into the row segments' (a half the boundary does not
+    // cross lies in one segment)
+    const bool halfA = rsplit > wr0;
 #pragma unroll
-      for (int nb = 0; nb < kBlocks; ++nb) colB[nb] = wc0 + nb * 32 + lr >= csplit;
-      {
-        float rv[32];
-#pragma unroll
-        for (int m2 = 0; m2 < 2; ++m2)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            float m = inf;
-#pragma unroll
-            for (int nb = 0; nb < kBlocks; ++nb) m = nmin(m, colB[nb] ? inf : d2[m2][nb][v]);
-            rv[m2 * 16 + v] = m;
-          }
-        rowminA = transpose_min32(rv, lr);
-      }
-      {
-        float rv[32];
-#pragma unroll
-        for (int m2 = 0; m2 < 2; ++m2)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            float m = inf;
-#pragma unroll
-            for (int nb = 0; nb < kBlocks; ++nb) m = nmin(m, colB[nb] ? d2[m2][nb][v] : inf);
-            rv[m2 * 16 + v] = m;
-          }
-        rowminB = transpose_min32(rv, lr);
+    for (int nb = 0; nb < kBlocks; ++nb) {
+      if constexpr (kRowSplit) {
+        cminA[nb] = nmin(cminA[nb], hA[nb]);
+        cminB[nb] = nmin(cminB[nb], hB[nb]);
+      } else {
+        cminA[nb] = nmin(cminA[nb], halfA ? hA[nb] : inf);
+        cminB[nb] = nmin(cminB[nb], halfA ? inf : hA[nb]);
       }
     }
     const bool rowInB = wr0 + transposed_row(lr, lh) >= rsplit;
     rmA[h] = (rowInB ? mBA : mAA) ? inf : rowminA;
     rmB[h] = (rowInB ? mBB : mAB) ? inf : rowminB;
-    if (unitw) {
+    if constexpr (kUnitRows) {
       rmA[h] = fmaf(kNegUnitScale, rmA[h], 2.f);
       rmB[h] = fmaf(kNegUnitScale, rmB[h], 2.f);
     }
+  };
+  using F = std::false_type;
+  using Tr = std::true_type;
+  auto run_half = [&](auto h_c) {
+    const int wr0 = wm * kWaveTile + decltype(h_c)::value * 64;
+    const bool rowsplit = rsplit > wr0 && rsplit < wr0 + 64;  // the row boundary crosses this half
+    if (unitw) {
+      if (!rowsplit && !colsplit)
+        reduce_half(h_c, Tr{}, F{}, F{});
+      else if (!colsplit)
+        reduce_half(h_c, Tr{}, Tr{}, F{});
+      else if (!rowsplit)
+        reduce_half(h_c, Tr{}, F{}, Tr{});
+      else
+        reduce_half(h_c, Tr{}, Tr{}, Tr{});
+    } else {
+      reduce_half(h_c, F{}, Tr{}, Tr{});  // rows not normalised: every distance selected
+    }
+  };
+  run_half(std::integral_constant<int, 0>{});
+  run_half(std::integral_constant<int, 1>{});
+  // column wc0 + (2q + lh) * 32 + lr: minima over the wave's 128 rows, per row segment
+  float cmA[2], cmB[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    cmA[q] = halves_min2(cminA[2 * q], cminA[2 * q + 1]);
+    cmB[q] = halves_min2(cminB[2 * q], cminB[2 * q + 1]);
   }
   if (unitw) {
 #pragma unroll
@@ -657,7 +640,7 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
     if (colInB ? mAB : mAA) cmA[q] = inf;
     if (colInB ? mBB : mBA) cmB[q] = inf;
   }
-  __syncthreads();  // the stash is no longer read
+  __syncthreads();  // operand buffers are no longer read
   float* s_cminA = reinterpret_cast<float*>(smem);  // [2 (wm)][TM]
   float* s_cminB = s_cminA + 2 * TM;
   float* s_rminA = s_cminB + 2 * TM;                 // [2 (wn)][TM]
@@ -694,6 +677,7 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
       if (b != inf) atomicMin(minbits + (long long)r * n + cA + 1, min_key(b));
     }
   }
+  }  // epilogue indices
 }
 
 inline int nkb_of(int c) { return (c + 2 * KB - 1) / (2 * KB) * 2; }
