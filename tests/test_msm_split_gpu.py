@@ -100,17 +100,27 @@ def test_minima_vs_f64_bruteforce(device):
 # lane halves (rows lh*4 + e); 383 and 385 offsets next to the 128-row wave edge and the
 # 64-row half edge; 300 and 449 mixed.  The straddling tiles are reduced per image segment
 # in 64-row halves; every per-(row, image) minimum is checked, so a distance credited to
-# the wrong segment shows.
+# the wrong segment shows.  With the rows normalised in the kernel (rows of unequal norms
+# in, unit rows scored) the waves take the unit-row reduction, whose variants differ by
+# where the boundaries cross the wave; without, the general one.
+@pytest.mark.parametrize('normalize', [False, True])
 @pytest.mark.parametrize('p', [261, 264, 269, 300, 383, 385, 449])
-def test_minima_at_boundary_offsets_vs_f64_bruteforce(device, p):
+def test_minima_at_boundary_offsets_vs_f64_bruteforce(device, p, normalize):
     n = 8
     torch.manual_seed(p)
-    z = torch.nn.functional.normalize(torch.randn((n, p, 48)) + 0.3 * torch.randn((1, 1, 48)), dim=-1)
+    z = torch.randn((n, p, 48)) + 0.3 * torch.randn((1, 1, 48))
+    if normalize:
+        z = z * (0.5 + torch.rand((n, p, 1)))
+        z64 = z.double().numpy()
+        ref_in = (z64 / np.linalg.norm(z64, axis=-1, keepdims=True)).astype(np.float32)
+    else:
+        z = torch.nn.functional.normalize(z, dim=-1)
+        ref_in = z.numpy()
     offs = sorted({(k * p) % 256 for k in range(1, n)})
-    got = _split_minima(z.to(device), normalize=False)
-    ref = oracle.msm_nearest_f64_c(z.numpy()) ** 2
+    got = _split_minima(z.to(device), normalize=normalize)
+    ref = oracle.msm_nearest_f64_c(ref_in) ** 2
     fin = np.isfinite(ref)
-    print(f'p={p}: boundary offsets {offs}', flush=True)
+    print(f'p={p} normalize={normalize}: boundary offsets {offs}', flush=True)
     assert np.isinf(got[~fin]).all(), 'own-image entries must stay +inf'
     np.testing.assert_allclose(got[fin], ref[fin], rtol=0, atol=2e-6)
 
