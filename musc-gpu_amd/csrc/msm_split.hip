@@ -485,10 +485,12 @@ __global__ __launch_bounds__(THREADS, 1) void split_pair_kernel(const _Float16* 
   // padding) depends only on the two segments, so minima are taken per segment over
   // the raw distances and a masked segment pair becomes +inf afterwards.  Each 64-row
   // half of the wave is reduced in one pass over its accumulators, as in the one-pair
-  // case: only a half that the row boundary crosses sorts each distance into the
-  // column minima of its row's segment, and only a wave that the column boundary
-  // crosses sorts it into the row minima of its column's segment (a select per
-  // distance, so that a NaN distance of a masked pair cannot reach an unmasked minimum).
+  // case: with unit rows, only a half that the row boundary crosses sorts each distance
+  // into the column minima of its row's segment, and only a wave that the column
+  // boundary crosses sorts it into the row minima of its column's segment; with rows not
+  // normalised every distance is sorted both ways (one variant: more of them left the
+  // register allocator no room).  Sorting is a select per distance, so that a NaN
+  // distance of a masked pair cannot reach an unmasked minimum.
   const int rsplit = min(TM, min((rA + 1) * p, rows) - row0);
   const int csplit = min(TM, min((cA + 1) * p, rows) - col0);
   const int rBimg = row0 + rsplit < rows ? rA + 1 : n;  // used only when segment B is not empty
