@@ -48,6 +48,7 @@ namespace msm {
 namespace split {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 
 constexpr int TM = 256;                      // triangle tile: rows = columns, one workgroup per tile
 constexpr int KB = 16;                       // channels per stage (each of hi and lo)
@@ -85,7 +86,28 @@ __global__ __launch_bounds__(256) void split_prepare_kernel(const float* __restr
   const long long row = (long long)blockIdx.x * (blockDim.x / kWave) + wave;
   if (row >= rows) return;
   const float* src = z + row * (long long)c;
-  const double acc = row_sumsq(src, c, lane);
+  // A row of whole 32-channel pairs of blocks, up to 1024 channels (the pools' C), stays in
+  // registers between its norm and its split (at most 4 float4 per lane, taken by the same
+  // lanes in the same order as row_sumsq, so the same sum); otherwise the split reads the
+  // row again.
+  const bool in_regs = (c & 31) == 0 && c <= 16 * kWave;
+  float4 xv[4];
+  double acc = 0.0;
+  if (in_regs) {
+    const float4* s4 = reinterpret_cast<const float4*>(src);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = lane + j * kWave;
+      if (k < c / 4) {
+        const float4 v = s4[k];
+        xv[j] = v;
+        acc += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+      }
+    }
+    acc = wave_sum(acc);
+  } else {
+    acc = row_sumsq(src, c, lane);
+  }
   const double unit = ldexp(1.0, -kScaleShift);
   if (lane == 0) {
     float nrm;
@@ -104,12 +126,43 @@ __global__ __launch_bounds__(256) void split_prepare_kernel(const float* __restr
   const double sc = acc > 0.0 ? ldexp(1.0 / sqrt(acc), kScaleShift) : 0.0;
   _Float16* dst = hl + row * (long long)nkb * (2 * KB);
   const int cp = nkb * KB;
+  // hi = fp16(fp32(v)), lo = fp16(fp32(v - hi)) with v = x * sc rounded to fp64, each step
+  // rounded to nearest even as written: the empty asm statements keep the compiler from
+  // folding the two narrowing steps into one (a software f64 -> f16 rounding, which
+  // differs on ties of the fp32 step) or fusing x * sc into the subtraction, which it
+  // otherwise does in some paths and not in others.
   auto split1 = [&](float x, _Float16& hi, _Float16& lo) {
-    const double v = (double)x * sc;
-    hi = (_Float16)(float)v;
-    lo = (_Float16)(float)(v - (double)(float)hi);
+    double v = (double)x * sc;
+    asm volatile("" : "+v"(v));
+    float vf = (float)v;
+    asm volatile("" : "+v"(vf));
+    hi = (_Float16)vf;
+    float rf = (float)(v - (double)(float)hi);
+    asm volatile("" : "+v"(rf));
+    lo = (_Float16)rf;
   };
-  if ((c & 7) == 0) {
+  if (in_regs) {
+    // channels 4k .. 4k+3 (k = lane + j*64): one 8-byte store of hi and one of lo in
+    // block k / 4 (no padding channels: c is a multiple of 32)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = lane + j * kWave;
+      if (k < c / 4) {
+        const float xs[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+        half4 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          _Float16 h, l;
+          split1(xs[e], h, l);
+          hi[e] = h;
+          lo[e] = l;
+        }
+        _Float16* blk = dst + (k >> 2) * (2 * KB) + (k & 3) * 4;
+        *reinterpret_cast<half4*>(blk) = hi;
+        *reinterpret_cast<half4*>(blk + KB) = lo;
+      }
+    }
+  } else if ((c & 7) == 0) {
     // eight channels per lane: one 16-byte store of hi and one of lo (half a
     // 16-channel block each); c % 8 == 0 keeps every group inside one block
     for (int k0 = 8 * lane; k0 < cp; k0 += 8 * kWave) {
