@@ -125,6 +125,42 @@ def test_minima_at_boundary_offsets_vs_f64_bruteforce(device, p, normalize):
     np.testing.assert_allclose(got[fin], ref[fin], rtol=0, atol=2e-6)
 
 
+# The hi/lo split exactly as written -- hi = fp16(fp32(v)), lo = fp16(fp32(v - hi)), v =
+# x * 2^10 / ||row|| in fp64, each narrowing rounded to nearest even -- on the prepare
+# kernel's three paths (a row in registers: c a multiple of 32 up to 1024; eight channels
+# per lane; one), zero padding included.  Integer-valued rows make the fp64 sum of squares
+# exact in any order, so the restatement's scale is the kernel's bit for bit; a compiler
+# that folds the two narrowing steps into one rounding, or fuses x * scale into the
+# subtraction, changes some of these bits.
+@pytest.mark.parametrize('c', [1024, 96, 1000, 37])
+def test_split_array_rounding_as_written(device, c):
+    n, p = 2, 260
+    rng = np.random.default_rng(c)
+    z = rng.integers(-60, 61, size=(n, p, c)).astype(np.float32)
+    z *= np.exp2(rng.integers(-6, 7, size=(n, p, 1))).astype(np.float32)  # exact: powers of two
+    zt = torch.from_numpy(z).to(device)
+    ws = rt.workspace(_MSM_hip.workspace_bytes(n, p, c, 'split16'), device)
+    ws.zero_()
+    lib = rt.library()
+    rt.check(lib.musc_msm_split_prepare_f32(zt.data_ptr(), n, p, c, 0, ws.data_ptr(), ws.numel(), rt.stream(device)),
+             'prepare')
+    torch.cuda.synchronize()
+    rows, nkb = n * p, (c + 31) // 32 * 2
+    hl_bytes = rows * nkb * 64
+    off = ws.numel() - (hl_bytes + 255) // 256 * 256
+    got = ws[off:off + hl_bytes].cpu().numpy().view(np.uint16).reshape(rows, nkb, 2, 16)
+    x = np.zeros((rows, nkb * 16))
+    x[:, :c] = z.reshape(rows, c).astype(np.float64)
+    acc = (x * x).sum(axis=1)  # exact: integers below 2^53 times powers of four
+    sc = np.ldexp(1.0 / np.sqrt(acc), 10)
+    v = x * sc[:, None]
+    hi = v.astype(np.float32).astype(np.float16)
+    lo = (v - hi.astype(np.float64)).astype(np.float32).astype(np.float16)
+    want = np.stack([hi.reshape(rows, nkb, 16), lo.reshape(rows, nkb, 16)], axis=2).view(np.uint16)
+    bad = np.argwhere(got != want)
+    assert len(bad) == 0, f'{len(bad)} of {got.size} split values differ, first (row, block, hi/lo, k) {bad[:4].tolist()}'
+
+
 def test_config1_plumbing_kernel_level(device):
     z = synthetic.msm_features(8, 1369, 1024, seed=42)
     zd = z.to(device)
