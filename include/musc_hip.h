@@ -146,8 +146,9 @@ int musc_msm_rank_f32(int n, int p, int rank_lo, int rank_hi, double* scores,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Split engine: the same scores, with each fp32 dot product formed from three
- * fp16 MFMA products.  Rows are L2-normalised and scaled by 2^10, split as
- * hi = fp16(v), lo = fp16(v - hi), and a.b is accumulated in fp32 as
+ * fp16 MFMA products.  Rows are L2-normalised and scaled by 2^10 (v in fp64), split
+ * as hi = fp16(fp32(v)), lo = fp16(fp32(v - hi)) with every narrowing rounded to
+ * nearest even, and a.b is accumulated in fp32 as
  * hi.hi + hi.lo + lo.hi (error below 2^-22 |a||b|, the order of fp32's own
  * accumulation error); a per-row scale restores the units, so MUSC_MSM_NORMALIZE_ROWS
  * and unnormalised inputs both work.  Same contract, arguments and stage order as
